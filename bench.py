@@ -1,0 +1,288 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged-KV GQA decode operator (one GPU).
+
+A step is one decode call (partition kernel + LSE combine) over one batch of
+synthetic input already resident in HBM.  The default workload is BASELINE
+config C2 (Llama-3-8B decode shape: B 32, 32/8 heads, D 128, bf16, page 64,
+cache_seqlens U[512, 4096]).  Calls rotate over `--sets` independent KV pools
+so the per-call working set is never the previous call's (MI355X has a 256 MB
+MALL).  Prints ONE JSON line on stdout.
+
+    python bench.py [--steps K] [--warmup W] [--config c2] [--sets 3]
+                    [--path 0|1|2] [--splits N] [--all] [--json-out FILE]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "flashatte-hand_amd"))
+
+METRIC = "KV-stream HBM GB/s (% of MI355X peak) and µs/decode call, 8B GQA shape"
+HBM_PEAK_GBPS = 8000.0  # MI355X published HBM3E bandwidth
+
+
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime torch already loaded."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n: int):
+        evs = (ctypes.c_void_p * n)()
+        for i in range(n):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            evs[i] = e
+        return evs
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(ms.value)
+
+    def destroy(self, evs):
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+
+
+def percentile(xs, p):
+    xs = sorted(xs)
+    if not xs:
+        return None
+    k = (len(xs) - 1) * p / 100.0
+    lo, hi = int(math.floor(k)), int(math.ceil(k))
+    return xs[lo] + (xs[hi] - xs[lo]) * (k - lo)
+
+
+def load_traffic(cfg_name: str, path_name: str):
+    """HBM bytes per partition launch from the committed rocprofv3 PMC summary, if present."""
+    f = REPO / "profiles" / f"pmc_{cfg_name}_{path_name}.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return float(d["hbm_bytes_per_dispatch"])
+    except Exception:
+        return None
+
+
+def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
+    from pagedkv.configs import make_config, make_tensors
+
+    cfg = make_config(name)
+    sets = [make_tensors(cfg, "cuda", seed=cfg.seed + 7919 * i) for i in range(max(1, args.sets))]
+    torch.cuda.synchronize()
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    D = cfg.head_dim
+    base = sets[0]
+    desc = pagedkv.make_desc(
+        batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k, head_dim=D,
+        page_size=cfg.page_size, num_pages=base["k_cache"].shape[0], block_table_stride=cfg.block_table.shape[1],
+        dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
+        max_seqlen=int(cfg.seqlens.max()), path=args.path,
+    )
+    splits_req = args.splits if args.splits is not None else cfg.num_splits
+    splits = pagedkv.num_splits_for(desc, splits_req)
+    path = pagedkv.path_for(desc)
+    ws_bytes = pagedkv.workspace_size(desc, splits_req)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    desc.workspace = ws.data_ptr()
+    desc.workspace_bytes = ws_bytes
+    outs = [torch.empty_like(s["q"]) for s in sets]
+    lib = pagedkv._lib.load()
+
+    ptrs = [(s["q"].data_ptr(), s["k_cache"].data_ptr(), s["v_cache"].data_ptr(), s["block_table"].data_ptr(),
+             s["cache_seqlens"].data_ptr(), o.data_ptr()) for s, o in zip(sets, outs)]
+    scale = float(cfg.scale)
+
+    def call(i, ev_ptr=None):
+        q, k, v, bt, sl, o = ptrs[i % len(ptrs)]
+        desc.prof_events = ev_ptr
+        st = lib.pkv_decode(q, k, v, bt, sl, scale, splits_req, o, ctypes.byref(desc), sh)
+        if st != 0:
+            raise pagedkv.PkvError(st)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+
+    # Timed region: K calls, per-call events around the partition kernel and the combine.
+    K = args.steps
+    evs = events.create(3 * K)
+    t_start, t_end = events.create(2)
+    torch.cuda.synchronize()
+    events.hip.hipEventRecord(t_start, sh)
+    for i in range(K):
+        call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p))
+    events.hip.hipEventRecord(t_end, sh)
+    torch.cuda.synchronize()
+    total_ms = events.elapsed_ms(t_start, t_end)
+    part_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) for i in range(K)]
+    comb_ms = [events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) for i in range(K)]
+    call_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 2]) for i in range(K)]
+    events.destroy(evs)
+    events.destroy([t_start, t_end])
+
+    ms_per_step = total_ms / K
+    kv_bytes = cfg.kv_bytes()
+    # Algorithmic bytes of one partition launch: valid K/V rows + q + block-table entries + seqlens
+    # (the output is written by the combine kernel and is not counted here).
+    part_alg = cfg.total_bytes() - cfg.batch * cfg.num_heads * D * cfg.elem_bytes
+    part_avg_ms = sum(part_ms) / K
+    achieved = part_alg / (part_avg_ms * 1e-3) / 1e9
+    traffic = load_traffic(name, "mfma" if path == pagedkv.PKV_PATH_MFMA else "valu")
+    res = {
+        "config": cfg,
+        "ms_per_step": ms_per_step,
+        "kv_gbps": kv_bytes / (ms_per_step * 1e-3) / 1e9,
+        "total_gbps": cfg.total_bytes() / (ms_per_step * 1e-3) / 1e9,
+        "us_p10": percentile(call_ms, 10) * 1e3,
+        "us_p50": percentile(call_ms, 50) * 1e3,
+        "us_p90": percentile(call_ms, 90) * 1e3,
+        "partition_us": part_avg_ms * 1e3,
+        "combine_us": sum(comb_ms) / K * 1e3,
+        "splits": splits,
+        "path": {1: "valu", 2: "mfma"}.get(path, str(path)),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "partition",
+            "alg_bytes_per_launch": int(part_alg),
+        },
+        "host_arrays": (base, cfg),
+    }
+    return res
+
+
+def cpu_baseline(res: dict, torch, budget_s: float) -> dict:
+    """The oracle's fp32 restatement of the reference's scalar decode on the host cores."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import numpy as np
+
+    import pkv_oracle as po
+
+    base, cfg = res["host_arrays"]
+    q = base["q"].view(torch.int16).cpu().numpy().view(np.uint16)
+    k = base["k_cache"].view(torch.int16).cpu().numpy().view(np.uint16)
+    v = base["v_cache"].view(torch.int16).cpu().numpy().view(np.uint16)
+    dt = 0 if cfg.dtype == "f16" else 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        a = time.perf_counter()
+        po.decode_f32(q, k, v, cfg.block_table, cfg.seqlens, cfg.scale, dt, threads=threads)
+        times.append(time.perf_counter() - a)
+        if time.perf_counter() - t0 >= budget_s or len(times) >= 1000:
+            break
+    t = sorted(times)[len(times) // 2]
+    return {
+        "value": round(cfg.kv_bytes() / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} full {cfg.name} calls (median {t * 1e3:.1f} ms/call), fp32 online-softmax "
+                  f"restatement of best_flashattn_kvcache_decode.cu:233-371, OpenMP over (b, h)",
+        "us_per_call": round(t * 1e6, 1),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--sets", type=int, default=3, help="independent KV pools rotated across calls")
+    ap.add_argument("--path", type=int, default=0, help="0 auto, 1 VALU, 2 MFMA")
+    ap.add_argument("--splits", type=int, default=None, help="num_splits (default: the config's, 0 = heuristic)")
+    ap.add_argument("--all", action="store_true", help="also measure every other config (extra lines to --json-out)")
+    ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(decode shards with no communication; see DESIGN.md).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import pagedkv
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    events = HipEvents()
+    names = [args.config] + ([n for n in ("c1", "c2", "c3", "c4", "c5") if n != args.config] if args.all else [])
+    lines = []
+    headline = None
+    for name in names:
+        res = run_config(name, args, torch, pagedkv, events)
+        cfg = res["config"]
+        line = {
+            "metric": METRIC,
+            "value": round(res["kv_gbps"], 1),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(res["ms_per_step"], 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": cfg.dtype,
+            "data": "synthetic (seeded N(0,1) values, random paged layout; see pagedkv/configs.py)",
+            "config": {**cfg.describe(), "splits": res["splits"], "path": res["path"], "kv_sets": args.sets},
+            "us_per_call": round(res["ms_per_step"] * 1e3, 2),
+            "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
+            "hbm_frac_kv": round(res["kv_gbps"] / HBM_PEAK_GBPS, 4),
+            "total_alg_gbps": round(res["total_gbps"], 1),
+            "partition_us": round(res["partition_us"], 2),
+            "combine_us": round(res["combine_us"], 2),
+            "roofline": res["roofline"],
+            "cpu_baseline": None,
+        }
+        if name == args.config and not args.no_cpu:
+            line["cpu_baseline"] = cpu_baseline(res, torch, args.cpu_budget)
+        res.pop("host_arrays", None)
+        lines.append(line)
+        if headline is None:
+            headline = line
+        print(f"[bench] {name}: {line['us_per_call']} us/call, {line['value']} GB/s KV "
+              f"({100 * line['hbm_frac_kv']:.1f}% of peak), partition {line['partition_us']} us "
+              f"({100 * line['roofline']['frac']:.1f}% roofline), combine {line['combine_us']} us, "
+              f"splits {res['splits']}, path {res['path']}", file=sys.stderr, flush=True)
+        del res
+        torch.cuda.empty_cache()
+    if args.json_out:
+        with open(args.json_out, "a") as f:
+            for ln in lines:
+                f.write(json.dumps(ln) + "\n")
+    print(json.dumps(headline), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

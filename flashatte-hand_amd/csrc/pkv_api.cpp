@@ -1,0 +1,334 @@
+// pkv_api.cpp — C ABI of the gfx950 paged-KV decode operator (include/pkv_decode.h).
+//
+// Host dispatch: validate -> resolve split count -> check workspace -> launch
+// the partition kernel (VALU or MFMA family) -> launch the LSE combine when
+// splits > 1.  Replaces the reference's run_kernel dispatch
+// (submission-oj/best_flashattn_kvcache_decode.cu:1186-1426), which validated
+// by silent return, chose splits from a (B, seqlen_k) table and owned a hidden
+// workspace.  Here every failure is a status code, the caller owns the
+// workspace, and all work is enqueued on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <mutex>
+
+#include "../../include/pkv_decode.h"
+#include "pkv_launch.h"
+
+namespace {
+
+// gfx950 (MI355X) compute units; the split heuristic sizes grids against it.
+constexpr int kComputeUnits = 256;
+// Work items (waves) per CU the heuristic aims for: enough independent
+// 16-byte/lane streams in flight to cover HBM latency.
+constexpr int kTargetWavesPerCU = 16;
+// Shortest split worth a separate partial (tokens): below this the partial
+// O write + combine read outweigh the extra parallelism.
+constexpr int kMinTokensPerSplit = 256;
+
+struct Resolved {
+    int64_t B, H, Hk, D, P, group;
+    int page_shift;
+    int heads_per_wave;
+    int head_groups;
+    int path;
+    int64_t max_pages;
+};
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+int ilog2(int64_t x) {
+    int s = 0;
+    while ((int64_t{1} << s) < x) {
+        ++s;
+    }
+    return s;
+}
+
+int valu_heads_per_wave(int64_t group) {
+    if (group <= 1) return 1;
+    if (group <= 2) return 2;
+    if (group <= 4) return 4;
+    if (group <= 8) return 8;
+    return 16;
+}
+
+// Kernel family per shape.  Chosen from measurements on MI355X (bench.py
+// --sweep-paths): MFMA for every group size it supports.
+int auto_path(const Resolved& r) {
+    (void)r;
+    return PKV_PATH_MFMA;
+}
+
+// Validates the descriptor; fills `r`.  Returns PKV_OK or an error status.
+int resolve(const pkv_decode_desc* d, Resolved& r) {
+    if (d == nullptr) {
+        return PKV_EINVAL;
+    }
+    if (d->batch <= 0 || d->num_heads <= 0 || d->num_heads_k <= 0 || d->num_pages <= 0 ||
+        d->block_table_stride <= 0 || d->max_seqlen < 0) {
+        return PKV_EINVAL;
+    }
+    if (d->num_heads % d->num_heads_k != 0) {
+        return PKV_EINVAL;
+    }
+    if (d->dtype != PKV_DTYPE_F16 && d->dtype != PKV_DTYPE_BF16) {
+        return PKV_EUNSUPPORTED;
+    }
+    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) {
+        return PKV_EUNSUPPORTED;
+    }
+    if (!is_pow2(d->page_size) || d->page_size > 1024) {
+        return PKV_EUNSUPPORTED;
+    }
+    if (d->path != PKV_PATH_AUTO && d->path != PKV_PATH_VALU && d->path != PKV_PATH_MFMA) {
+        return PKV_EINVAL;
+    }
+    // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.
+    if (d->batch * d->num_heads > (int64_t{1} << 30) || d->num_pages > INT32_MAX ||
+        d->block_table_stride > INT32_MAX) {
+        return PKV_EUNSUPPORTED;
+    }
+    r.B = d->batch;
+    r.H = d->num_heads;
+    r.Hk = d->num_heads_k;
+    r.D = d->head_dim;
+    r.P = d->page_size;
+    r.group = r.H / r.Hk;
+    r.page_shift = ilog2(r.P);
+    const int64_t row_cap = d->block_table_stride * r.P;
+    const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
+    r.max_pages = std::max<int64_t>(1, (max_seqlen + r.P - 1) / r.P);
+    r.path = d->path == PKV_PATH_AUTO ? auto_path(r) : d->path;
+    r.heads_per_wave = r.path == PKV_PATH_MFMA ? 16 : valu_heads_per_wave(r.group);
+    r.head_groups = static_cast<int>((r.group + r.heads_per_wave - 1) / r.heads_per_wave);
+    return PKV_OK;
+}
+
+// Split count: aim for kTargetWavesPerCU waves per CU across the whole grid,
+// but never below kMinTokensPerSplit tokens per split of the longest row and
+// never more splits than that row has pages (or PKV_MAX_SPLITS).  Unlike the
+// reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
+// it counts KV heads, head groups and the CU count of the part.
+int choose_splits(const Resolved& r, int64_t max_seqlen) {
+    const int64_t items = r.B * r.Hk * r.head_groups;
+    const int64_t target = int64_t{kComputeUnits} * kTargetWavesPerCU;
+    int64_t s = (target + items - 1) / items;
+    const int64_t by_len = std::max<int64_t>(1, max_seqlen / kMinTokensPerSplit);
+    s = std::min(s, by_len);
+    s = std::min<int64_t>(s, r.max_pages);
+    s = std::min<int64_t>(s, PKV_MAX_SPLITS);
+    return static_cast<int>(std::max<int64_t>(1, s));
+}
+
+int resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
+    if (num_splits < 0) {
+        return 0;
+    }
+    const int64_t row_cap = d->block_table_stride * r.P;
+    const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
+    int64_t s = num_splits == 0 ? choose_splits(r, max_seqlen) : num_splits;
+    s = std::min<int64_t>(s, r.max_pages);
+    s = std::min<int64_t>(s, PKV_MAX_SPLITS);
+    return static_cast<int>(std::max<int64_t>(1, s));
+}
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+size_t workspace_bytes(const Resolved& r, int splits) {
+    if (splits <= 1) {
+        return 0;
+    }
+    const size_t rows = static_cast<size_t>(r.B * r.H) * static_cast<size_t>(splits);
+    return align_up(rows * static_cast<size_t>(r.D) * sizeof(float)) + align_up(rows * sizeof(float));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+thread_local int t_last_status = PKV_OK;
+
+// Library-owned grow-only workspace for the reference-compatible run_kernel
+// (the reference keeps the same kind of static buffer, best:17-20, 1078-1133).
+std::mutex g_legacy_mutex;
+void* g_legacy_ws = nullptr;
+size_t g_legacy_ws_bytes = 0;
+
+} // namespace
+
+extern "C" {
+
+const char* pkv_strerror(int status) {
+    switch (status) {
+    case PKV_OK: return "ok";
+    case PKV_EINVAL: return "invalid argument";
+    case PKV_EUNSUPPORTED: return "unsupported shape or dtype";
+    case PKV_ENOWORKSPACE: return "workspace missing or too small";
+    case PKV_ELAUNCH: return "HIP launch failed";
+    default: return "unknown status";
+    }
+}
+
+int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits);
+}
+
+int pkv_decode_path(const pkv_decode_desc* desc) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return r.path;
+}
+
+size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    const int splits = resolve_splits(desc, r, num_splits);
+    return workspace_bytes(r, splits);
+}
+
+int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+               const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
+               const pkv_decode_desc* desc, void* stream) {
+    Resolved r;
+    int st = resolve(desc, r);
+    if (st != PKV_OK) {
+        return st;
+    }
+    if (q == nullptr || k_cache == nullptr || v_cache == nullptr || block_table == nullptr ||
+        cache_seqlens == nullptr || out == nullptr) {
+        return PKV_EINVAL;
+    }
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out)) {
+        return PKV_EINVAL;
+    }
+    if (num_splits < 0 || !std::isfinite(softmax_scale)) {
+        return PKV_EINVAL;
+    }
+    const int splits = resolve_splits(desc, r, num_splits);
+    const size_t need = workspace_bytes(r, splits);
+    if (need > 0 && (desc->workspace == nullptr || desc->workspace_bytes < need || !aligned16(desc->workspace))) {
+        return PKV_ENOWORKSPACE;
+    }
+    const int64_t items = r.B * r.Hk * r.head_groups * splits;
+    if (items > INT32_MAX) {
+        return PKV_EUNSUPPORTED;
+    }
+
+    pkv::PartitionParams p{};
+    p.q = static_cast<const uint16_t*>(q);
+    p.k = static_cast<const uint16_t*>(k_cache);
+    p.v = static_cast<const uint16_t*>(v_cache);
+    p.block_table = block_table;
+    p.seqlens = cache_seqlens;
+    p.out = static_cast<uint16_t*>(out);
+    const size_t rows = static_cast<size_t>(r.B * r.H) * static_cast<size_t>(splits);
+    p.part_o = need > 0 ? static_cast<float*>(desc->workspace) : nullptr;
+    p.part_lse = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(desc->workspace) +
+                                                     align_up(rows * static_cast<size_t>(r.D) * sizeof(float)))
+                          : nullptr;
+    p.token_stride = r.Hk * r.D;
+    p.page_stride = r.P * r.Hk * r.D;
+    p.num_heads = static_cast<int32_t>(r.H);
+    p.num_heads_k = static_cast<int32_t>(r.Hk);
+    p.group = static_cast<int32_t>(r.group);
+    p.head_groups = r.head_groups;
+    p.splits = splits;
+    p.page_shift = r.page_shift;
+    p.bt_stride = static_cast<int32_t>(desc->block_table_stride);
+    p.num_pages = static_cast<int32_t>(desc->num_pages);
+    p.row_cap = static_cast<int32_t>(std::min<int64_t>(desc->block_table_stride * r.P, INT32_MAX));
+    p.num_items = static_cast<int32_t>(items);
+    p.scale_log2 = softmax_scale * 1.4426950408889634074f;
+
+    const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipEvent_t* ev = static_cast<hipEvent_t*>(desc->prof_events);
+
+    if (ev != nullptr && hipEventRecord(ev[0], s) != hipSuccess) {
+        return PKV_ELAUNCH;
+    }
+    hipError_t e = r.path == PKV_PATH_MFMA
+                       ? pkv::launch_partition_mfma(p, bf16, static_cast<int>(r.D), s)
+                       : pkv::launch_partition_valu(p, bf16, static_cast<int>(r.D), r.heads_per_wave, s);
+    if (e != hipSuccess) {
+        return PKV_ELAUNCH;
+    }
+    if (ev != nullptr && hipEventRecord(ev[1], s) != hipSuccess) {
+        return PKV_ELAUNCH;
+    }
+    if (splits > 1) {
+        pkv::CombineParams c{};
+        c.part_o = p.part_o;
+        c.part_lse = p.part_lse;
+        c.out = p.out;
+        c.rows = static_cast<int32_t>(r.B * r.H);
+        c.splits = splits;
+        if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s) != hipSuccess) {
+            return PKV_ELAUNCH;
+        }
+    }
+    if (ev != nullptr && hipEventRecord(ev[2], s) != hipSuccess) {
+        return PKV_ELAUNCH;
+    }
+    return PKV_OK;
+}
+
+void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_paged, void* output,
+                const int32_t* cache_seqlens, const int32_t* block_table, int64_t batch_size, int64_t seqlen_k,
+                int64_t seqlen_q, int64_t num_heads, int64_t num_heads_k, int64_t headdim, int64_t page_block_size,
+                int64_t num_blocks, int64_t causal) {
+    if (seqlen_q != 1 || causal != 0) {
+        t_last_status = PKV_EUNSUPPORTED;
+        return;
+    }
+    if (batch_size <= 0 || num_blocks < batch_size) {
+        t_last_status = PKV_EINVAL;
+        return;
+    }
+    pkv_decode_desc d{};
+    d.batch = batch_size;
+    d.num_heads = num_heads;
+    d.num_heads_k = num_heads_k;
+    d.head_dim = headdim;
+    d.page_size = page_block_size;
+    d.num_pages = num_blocks;
+    d.block_table_stride = num_blocks / batch_size; // best_flashattn_kvcache_decode.cu:1213-1215
+    d.max_seqlen = seqlen_k > 0 ? seqlen_k : 0;
+    d.dtype = PKV_DTYPE_BF16;
+    d.path = PKV_PATH_AUTO;
+
+    std::lock_guard<std::mutex> lock(g_legacy_mutex);
+    const size_t need = pkv_decode_workspace_size(&d, 0);
+    if (need > g_legacy_ws_bytes) {
+        void* fresh = nullptr;
+        if (hipMalloc(&fresh, need) != hipSuccess) {
+            t_last_status = PKV_ENOWORKSPACE;
+            return;
+        }
+        if (g_legacy_ws != nullptr) {
+            (void)hipFree(g_legacy_ws);
+        }
+        g_legacy_ws = fresh;
+        g_legacy_ws_bytes = need;
+    }
+    d.workspace = g_legacy_ws;
+    d.workspace_bytes = g_legacy_ws_bytes;
+    const float scale = 1.0f / std::sqrt(static_cast<float>(headdim > 0 ? headdim : 1));
+    t_last_status = pkv_decode(q, k_cache_paged, v_cache_paged, block_table, cache_seqlens, scale, 0, output, &d,
+                               nullptr);
+}
+
+int pkv_last_status(void) { return t_last_status; }
+
+} // extern "C"

@@ -1,0 +1,89 @@
+"""Build recipe for the gfx950 library ``libpkv_decode.so`` and the CPU oracle.
+
+The HIP sources are compiled with hipcc for gfx950 only, one object per source
+(in parallel), then linked into ``flashatte-hand_amd/lib/libpkv_decode.so``.
+Packed-fp32 VALU instructions are disabled for all device code
+(``-packed-fp32-ops``).  The oracle (test infrastructure) is built with its own
+Makefile into ``oracle/libpkv_oracle.so``.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent.parent          # flashatte-hand_amd/
+REPO_ROOT = PKG_ROOT.parent
+CSRC = PKG_ROOT / "csrc"
+BUILD_DIR = PKG_ROOT / "_build"
+LIB_DIR = PKG_ROOT / "lib"
+LIB_PATH = LIB_DIR / "libpkv_decode.so"
+ORACLE_DIR = REPO_ROOT / "oracle"
+ORACLE_LIB = ORACLE_DIR / "libpkv_oracle.so"
+
+SOURCES = ["pkv_valu.hip", "pkv_mfma.hip", "pkv_combine.hip", "pkv_api.cpp"]
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libpkv_decode.so)")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; that is harmless.
+    out = "\n".join(line for line in res.stdout.splitlines() if "packed-fp32-ops" not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{out}")
+    if verbose and out.strip():
+        print(out, flush=True)
+
+
+def build_library(verbose: bool = False, jobs: int = 4) -> Path:
+    """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds)."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    objs = []
+    cmds = []
+    for src in SOURCES:
+        obj = BUILD_DIR / (src.rsplit(".", 1)[0] + ".o")
+        lang = ["-x", "hip"]
+        cmds.append([hipcc, *HIPCC_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_oracle(verbose: bool = False) -> Path:
+    """Build the CPU oracle (test infrastructure) with its Makefile."""
+    cmd = ["make", "-s", "-B", "-C", str(ORACLE_DIR)]
+    _run(cmd, verbose)
+    return ORACLE_LIB
+
+
+if __name__ == "__main__":
+    import sys
+
+    v = "-v" in sys.argv
+    print(build_library(verbose=v))
+    print(build_oracle(verbose=v))

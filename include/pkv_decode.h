@@ -1,0 +1,128 @@
+/*
+ * pkv_decode.h — C ABI of the MI355X (gfx950) paged-KV GQA flash-attention
+ * decode operator.
+ *
+ * Every entry point takes plain pointers and sizes; nothing here depends on
+ * torch or on HIP headers (streams and events are passed as `void*` holding a
+ * hipStream_t / hipEvent_t).
+ *
+ * Tensor layouts (identical to the reference's flash-attn layout,
+ * scripts/evaluate_flashattn_submission.py:127-143, 249):
+ *   q, out         [B, 1, H, D]           16-bit (fp16 or bf16), contiguous
+ *   k_cache,
+ *   v_cache        [num_pages, P, Hk, D]  16-bit, contiguous
+ *   block_table    [B, block_table_stride] int32 physical page ids
+ *   cache_seqlens  [B]                    int32 valid tokens per row
+ * Token t of row b lives in page block_table[b][t / P], slot t % P; only
+ * t < cache_seqlens[b] is read.  Query head h reads KV head h / (H / Hk).
+ */
+#ifndef PKV_DECODE_H
+#define PKV_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The reference's run_kernel returns void and silently
+ * ignores unsupported shapes (submission-oj/best_flashattn_kvcache_decode.cu:1202-1211);
+ * every entry point here reports what happened instead. */
+#define PKV_OK 0
+#define PKV_EINVAL 1           /* null pointer, non-positive or inconsistent dims, misaligned pointer */
+#define PKV_EUNSUPPORTED 2     /* dtype / head_dim / page size / seqlen_q / causal not supported */
+#define PKV_ENOWORKSPACE 3     /* workspace missing or smaller than pkv_decode_workspace_size() */
+#define PKV_ELAUNCH 4          /* a HIP launch or runtime call failed */
+
+#define PKV_DTYPE_F16 0
+#define PKV_DTYPE_BF16 1
+
+/* Kernel family selector (pkv_decode_desc.path). */
+#define PKV_PATH_AUTO 0        /* measured choice per shape */
+#define PKV_PATH_VALU 1        /* VALU dot2 products + DPP row reductions */
+#define PKV_PATH_MFMA 2        /* gfx950 16x16x32 / 16x16x16 MFMA for QK^T and PV */
+
+/* Largest split count a single call may use (the reference caps at 64,
+ * best_flashattn_kvcache_decode.cu:15). */
+#define PKV_MAX_SPLITS 256
+
+typedef struct pkv_decode_desc {
+    int64_t batch;              /* B */
+    int64_t num_heads;          /* H, query heads */
+    int64_t num_heads_k;        /* Hk, KV heads; H % Hk == 0 */
+    int64_t head_dim;           /* D: 64, 128 or 256 */
+    int64_t page_size;          /* P: tokens per page, a power of two in [1, 1024] */
+    int64_t num_pages;          /* physical pages held by k_cache / v_cache */
+    int64_t block_table_stride; /* int32 elements between consecutive block_table rows */
+    int64_t max_seqlen;         /* host-known upper bound of cache_seqlens (flash-attn's seqlen_k);
+                                   0 = block_table_stride * page_size.  Used only to choose splits. */
+    int32_t dtype;              /* PKV_DTYPE_F16 or PKV_DTYPE_BF16 (q, caches and out share it) */
+    int32_t path;               /* PKV_PATH_* */
+    void* workspace;            /* device memory for split partials; may be NULL when splits == 1 */
+    size_t workspace_bytes;
+    void* prof_events;          /* optional: hipEvent_t[3] recorded before the partition kernel,
+                                   after it and after the combine kernel (profiling only; NULL in use) */
+} pkv_decode_desc;
+
+/*
+ * Paged-KV decode attention, seqlen_q = 1, non-causal:
+ *   out[b,h,:] = softmax(softmax_scale * q[b,h,:] . K[b,kvh,t,:]) V[b,kvh,t,:]  over t < cache_seqlens[b]
+ * Replaces the reference's `extern "C" void run_kernel(...)` launch entry
+ * (submission-oj/best_flashattn_kvcache_decode.cu:1186-1201) with the
+ * north-star argument order and an explicit stream.
+ *
+ * num_splits follows flash-attn (scripts/evaluate_flashattn_submission.py:246):
+ *   0 = heuristic, 1 = single pass writing `out` directly, n > 1 = forced
+ *   (clamped to [1, min(PKV_MAX_SPLITS, pages of max_seqlen)]).
+ * Rows with cache_seqlens[b] <= 0 produce zeros; a row with one token
+ * reproduces that token's V row bit-for-bit (best_flashattn_kvcache_decode.cu:256-283).
+ * Asynchronous on `stream` (NULL = the null stream); no host synchronisation.
+ * Reentrant when concurrent calls use distinct workspaces.
+ */
+int pkv_decode(const void* q, const void* k_cache, const void* v_cache,
+               const int32_t* block_table, const int32_t* cache_seqlens,
+               float softmax_scale, int num_splits, void* out,
+               const pkv_decode_desc* desc, void* stream);
+
+/* Bytes of workspace pkv_decode needs for this shape and num_splits (after
+ * the same heuristic/clamping pkv_decode applies).  Replaces the reference's
+ * hidden grow-only workspace (best_flashattn_kvcache_decode.cu:17-20, 1078-1133). */
+size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits);
+
+/* Split count pkv_decode will use for `num_splits` (0 = heuristic).
+ * Replaces choose_splits (best_flashattn_kvcache_decode.cu:1039-1076, 1299-1312).
+ * Returns 0 if desc is invalid. */
+int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits);
+
+/* Kernel family pkv_decode will use for this desc (resolves PKV_PATH_AUTO). */
+int pkv_decode_path(const pkv_decode_desc* desc);
+
+/* Human-readable name of a status code. */
+const char* pkv_strerror(int status);
+
+/*
+ * Drop-in for the reference's launch entry, same 15 arguments and meaning
+ * (submission-oj/best_flashattn_kvcache_decode.cu:1186-1201;
+ * scripts/evaluate_flashattn_submission.py:29-44): bf16 tensors,
+ * softmax_scale = 1/sqrt(headdim), heuristic splits, null stream,
+ * block_table row stride = num_blocks / batch_size, seqlen_k = max seqlen.
+ * Like the reference it keeps a grow-only workspace owned by the library
+ * and is therefore not reentrant.  Its status is available from
+ * pkv_last_status() instead of being dropped.
+ */
+void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_paged,
+                void* output, const int32_t* cache_seqlens, const int32_t* block_table,
+                int64_t batch_size, int64_t seqlen_k, int64_t seqlen_q, int64_t num_heads,
+                int64_t num_heads_k, int64_t headdim, int64_t page_block_size,
+                int64_t num_blocks, int64_t causal);
+
+/* Status of the calling thread's most recent run_kernel call.  No
+ * counterpart in the reference, whose run_kernel discards it. */
+int pkv_last_status(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKV_DECODE_H */

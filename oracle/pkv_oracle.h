@@ -1,0 +1,77 @@
+/*
+ * pkv_oracle.h — CPU oracle for the paged-KV GQA decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the
+ * checker (or as the timed CPU baseline).  The product path never calls it.
+ *
+ * Layouts are those of include/pkv_decode.h.  16-bit tensors are passed as
+ * uint16_t bit patterns; dtype 0 = fp16, 1 = bf16.
+ */
+#ifndef PKV_ORACLE_H
+#define PKV_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct pkv_oracle_dims {
+    int64_t batch;
+    int64_t num_heads;
+    int64_t num_heads_k;
+    int64_t head_dim;
+    int64_t page_size;
+    int64_t num_pages;
+    int64_t block_table_stride;
+    int32_t dtype;
+    int32_t num_threads; /* OpenMP threads; <= 0 = runtime default */
+} pkv_oracle_dims;
+
+/* 16-bit <-> fp32 conversions written from the IEEE 754 / bfloat16 definitions
+ * (round-to-nearest-even, NaN kept quiet). */
+float pkv_oracle_f16_to_f32(uint16_t h);
+uint16_t pkv_oracle_f32_to_f16(float f);
+float pkv_oracle_bf16_to_f32(uint16_t h);
+uint16_t pkv_oracle_f32_to_bf16(float f);
+
+/* Restatement of the reference's generic scalar decode
+ * (submission-oj/best_flashattn_kvcache_decode.cu:233-371): per (b, h), per
+ * token, fp32 online softmax in natural-exp units, output cast RNE.
+ * Also the timed CPU baseline. */
+void pkv_oracle_decode_f32(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, const int32_t* block_table,
+                           const int32_t* cache_seqlens, float softmax_scale, uint16_t* out);
+
+/* Textbook dense attention in fp64 on the gathered K/V rows
+ * (the reference's own check formula, submission-oj/diagnostics/diag_integrated.py:49-57).
+ * out is fp64 [B, H, D]; rows with seqlen <= 0 give zeros. */
+void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, const int32_t* block_table,
+                           const int32_t* cache_seqlens, double softmax_scale, double* out);
+
+/* Split-KV partition step (best_flashattn_kvcache_decode.cu:664-697, 782-864):
+ * split s of row b covers pages [n*s/S, n*(s+1)/S) of its n valid pages;
+ * exp2-domain fp32 online softmax; part_o [B*H*S, D] normalised, part_lse
+ * [B*H*S] = m2 + log2(sum) or -inf when empty (O = 0 then). */
+void pkv_oracle_split_partials(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                               const uint16_t* v_cache, const int32_t* block_table,
+                               const int32_t* cache_seqlens, float softmax_scale, int splits,
+                               float* part_o, float* part_lse);
+
+/* LSE combine (best_flashattn_kvcache_decode.cu:956-1037, v11:604-613):
+ * w_s = exp2(lse_s - max) (0 for -inf), out = (sum_s w_s o_s) * (1 / sum_s w_s),
+ * o_s never read when w_s == 0.  out is 16-bit [rows, D]. */
+void pkv_oracle_combine(const float* part_o, const float* part_lse, int64_t rows, int splits,
+                        int64_t head_dim, int32_t dtype, uint16_t* out);
+
+/* Same combine with an fp32 result (for split-invariance checks before the cast). */
+void pkv_oracle_combine_f32(const float* part_o, const float* part_lse, int64_t rows, int splits,
+                            int64_t head_dim, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKV_ORACLE_H */

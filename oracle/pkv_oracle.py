@@ -1,0 +1,163 @@
+"""ctypes binding of the CPU oracle ``oracle/libpkv_oracle.so``.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker (or the timed CPU baseline).
+16-bit tensors are numpy uint16 bit patterns; dtype 0 = fp16, 1 = bf16.
+Function-by-function reference citations are in pkv_oracle.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libpkv_oracle.so"
+
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("num_heads", ctypes.c_int64),
+        ("num_heads_k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("page_size", ctypes.c_int64),
+        ("num_pages", ctypes.c_int64),
+        ("block_table_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("num_threads", ctypes.c_int32),
+    ]
+
+
+_LIB = None
+
+
+def build() -> Path:
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def load():
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    dp = ctypes.POINTER(Dims)
+    lib.pkv_oracle_decode_f32.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_float, _u16p]
+    lib.pkv_oracle_decode_f32.restype = None
+    lib.pkv_oracle_decode_f64.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_double, _f64p]
+    lib.pkv_oracle_decode_f64.restype = None
+    lib.pkv_oracle_split_partials.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_float, ctypes.c_int,
+                                              _f32p, _f32p]
+    lib.pkv_oracle_split_partials.restype = None
+    lib.pkv_oracle_combine.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int64, ctypes.c_int32,
+                                       _u16p]
+    lib.pkv_oracle_combine.restype = None
+    lib.pkv_oracle_combine_f32.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int64, _f32p]
+    lib.pkv_oracle_combine_f32.restype = None
+    for n in ("pkv_oracle_f16_to_f32", "pkv_oracle_bf16_to_f32"):
+        getattr(lib, n).argtypes = [ctypes.c_uint16]
+        getattr(lib, n).restype = ctypes.c_float
+    for n in ("pkv_oracle_f32_to_f16", "pkv_oracle_f32_to_bf16"):
+        getattr(lib, n).argtypes = [ctypes.c_float]
+        getattr(lib, n).restype = ctypes.c_uint16
+    _LIB = lib
+    return lib
+
+
+def dims(batch, num_heads, num_heads_k, head_dim, page_size, num_pages, block_table_stride, dtype, threads=0):
+    d = Dims()
+    d.batch, d.num_heads, d.num_heads_k, d.head_dim = batch, num_heads, num_heads_k, head_dim
+    d.page_size, d.num_pages, d.block_table_stride = page_size, num_pages, block_table_stride
+    d.dtype = dtype
+    d.num_threads = threads if threads else int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return d
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def _dims_from(q, k_cache, block_table, dtype, threads):
+    B, _, H, D = q.shape
+    num_pages, P, Hk, _ = k_cache.shape
+    return dims(B, H, Hk, D, P, num_pages, block_table.shape[1], dtype, threads)
+
+
+def decode_f32(q, k_cache, v_cache, block_table, seqlens, scale, dtype, threads=0):
+    """fp32 online-softmax restatement (best:233-371); returns uint16 [B,1,H,D]."""
+    lib = load()
+    d = _dims_from(q, k_cache, block_table, dtype, threads)
+    out = np.empty(q.shape, dtype=np.uint16)
+    lib.pkv_oracle_decode_f32(ctypes.byref(d), _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16),
+                              _c(block_table, np.int32), _c(seqlens, np.int32), float(scale), out)
+    return out
+
+
+def decode_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, threads=0):
+    """Dense fp64 softmax(q k^T scale) v on the gathered rows; returns float64 [B,1,H,D]."""
+    lib = load()
+    d = _dims_from(q, k_cache, block_table, dtype, threads)
+    out = np.empty(q.shape, dtype=np.float64)
+    lib.pkv_oracle_decode_f64(ctypes.byref(d), _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16),
+                              _c(block_table, np.int32), _c(seqlens, np.int32), float(scale), out)
+    return out
+
+
+def split_partials(q, k_cache, v_cache, block_table, seqlens, scale, dtype, splits, threads=0):
+    """Per-split normalised O [B*H*S, D] and log2 LSE [B*H*S] (best:664-697, 782-864)."""
+    lib = load()
+    d = _dims_from(q, k_cache, block_table, dtype, threads)
+    B, _, H, D = q.shape
+    part_o = np.empty((B * H * splits, D), dtype=np.float32)
+    part_lse = np.empty((B * H * splits,), dtype=np.float32)
+    lib.pkv_oracle_split_partials(ctypes.byref(d), _c(q, np.uint16), _c(k_cache, np.uint16),
+                                  _c(v_cache, np.uint16), _c(block_table, np.int32), _c(seqlens, np.int32),
+                                  float(scale), int(splits), part_o, part_lse)
+    return part_o, part_lse
+
+
+def combine(part_o, part_lse, rows, splits, head_dim, dtype):
+    lib = load()
+    out = np.empty((rows, head_dim), dtype=np.uint16)
+    lib.pkv_oracle_combine(_c(part_o, np.float32), _c(part_lse, np.float32), rows, splits, head_dim, dtype, out)
+    return out
+
+
+def combine_f32(part_o, part_lse, rows, splits, head_dim):
+    lib = load()
+    out = np.empty((rows, head_dim), dtype=np.float32)
+    lib.pkv_oracle_combine_f32(_c(part_o, np.float32), _c(part_lse, np.float32), rows, splits, head_dim, out)
+    return out
+
+
+# ------------------------------------------------------------------ numpy 16-bit helpers (independent of the C code)
+
+def bits_to_f32(bits: np.ndarray, dtype: int) -> np.ndarray:
+    bits = np.asarray(bits, dtype=np.uint16)
+    if dtype == 1:
+        return (bits.astype(np.uint32) << 16).view(np.float32)
+    return bits.view(np.float16).astype(np.float32)
+
+
+def f32_to_bits(x: np.ndarray, dtype: int) -> np.ndarray:
+    """RNE conversion written with numpy (fp16 via numpy's IEEE half cast)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == 1:
+        u = x.view(np.uint32).astype(np.uint64)
+        nan = (u & 0x7FFFFFFF) > 0x7F800000
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+        return r
+    return x.astype(np.float16).view(np.uint16)

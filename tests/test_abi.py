@@ -1,0 +1,135 @@
+"""The C ABI: libpkv_decode.so loads, exports every function include/pkv_decode.h
+declares, and its host-only logic (validation, split heuristic, workspace size)
+behaves — none of these calls touches a GPU."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import pagedkv
+from pagedkv import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "pkv_decode.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def base_desc(**kw):
+    d = dict(batch=32, num_heads=32, num_heads_k=8, head_dim=128, page_size=64, num_pages=3000,
+             block_table_stride=64, dtype=pagedkv.PKV_DTYPE_BF16, max_seqlen=4096)
+    d.update(kw)
+    return pagedkv.make_desc(**d)
+
+
+def test_status_strings():
+    assert _lib.strerror(0) == "ok"
+    assert "workspace" in _lib.strerror(3)
+    assert _lib.strerror(99) == "unknown status"
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("batch", 0, pagedkv.PKV_EINVAL),
+    ("num_heads", 30, pagedkv.PKV_EINVAL),           # not a multiple of Hk = 8
+    ("head_dim", 96, pagedkv.PKV_EUNSUPPORTED),
+    ("page_size", 48, pagedkv.PKV_EUNSUPPORTED),     # not a power of two
+    ("page_size", 2048, pagedkv.PKV_EUNSUPPORTED),
+    ("dtype", 7, pagedkv.PKV_EUNSUPPORTED),
+    ("num_pages", 0, pagedkv.PKV_EINVAL),
+    ("block_table_stride", 0, pagedkv.PKV_EINVAL),
+    ("path", 9, pagedkv.PKV_EINVAL),
+])
+def test_invalid_descriptors_are_rejected_before_any_launch(field, value, status):
+    lib = _lib.load()
+    d = base_desc(**{field: value})
+    # Non-null but never dereferenced pointers: validation fails before any use.
+    p = ctypes.c_void_p(16)
+    st = lib.pkv_decode(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None)
+    assert st == status
+    assert pagedkv.workspace_size(d, 0) == 0
+    assert pagedkv.num_splits_for(d, 0) == 0
+
+
+def test_null_and_misaligned_pointers_are_rejected():
+    lib = _lib.load()
+    d = base_desc()
+    p = ctypes.c_void_p(4096)
+    assert lib.pkv_decode(None, p, p, p, p, 0.1, 1, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+    assert lib.pkv_decode(ctypes.c_void_p(4098), p, p, p, p, 0.1, 1, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+    assert lib.pkv_decode(p, p, p, p, p, float("nan"), 1, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+    assert lib.pkv_decode(p, p, p, p, p, 0.1, -1, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+    assert lib.pkv_decode(p, p, p, p, p, 0.1, 1, p, None, None) == pagedkv.PKV_EINVAL
+
+
+def test_missing_workspace_is_reported():
+    lib = _lib.load()
+    d = base_desc()
+    p = ctypes.c_void_p(4096)
+    assert pagedkv.num_splits_for(d, 4) == 4
+    st = lib.pkv_decode(p, p, p, p, p, 0.1, 4, p, ctypes.byref(d), None)
+    assert st == pagedkv.PKV_ENOWORKSPACE
+    d.workspace = 4096
+    d.workspace_bytes = pagedkv.workspace_size(d, 4) - 1
+    assert lib.pkv_decode(p, p, p, p, p, 0.1, 4, p, ctypes.byref(d), None) == pagedkv.PKV_ENOWORKSPACE
+
+
+def test_workspace_size_formula():
+    d = base_desc()
+    for s in (1, 2, 8, 64):
+        got = pagedkv.workspace_size(d, s)
+        if s == 1:
+            assert got == 0
+            continue
+        rows = 32 * 32 * s
+        align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+        assert got == align(rows * 128 * 4) + align(rows * 4)
+
+
+def test_split_resolution():
+    d = base_desc()
+    assert pagedkv.num_splits_for(d, 1) == 1
+    assert pagedkv.num_splits_for(d, 7) == 7
+    assert pagedkv.num_splits_for(d, 10_000) == 64          # clamped to the pages of max_seqlen
+    d2 = base_desc(max_seqlen=100_000, block_table_stride=4096)
+    assert pagedkv.num_splits_for(d2, 10_000) == pagedkv.PKV_MAX_SPLITS
+    auto = pagedkv.num_splits_for(d, 0)
+    assert 1 <= auto <= 64
+    # short rows never split below the minimum split length
+    assert pagedkv.num_splits_for(base_desc(max_seqlen=200), 0) == 1
+    # tiny batch with a long context gets many splits, capped by PKV_MAX_SPLITS
+    many = pagedkv.num_splits_for(base_desc(batch=1, num_heads=8, num_heads_k=1, max_seqlen=131072,
+                                            block_table_stride=2048), 0)
+    assert 64 <= many <= pagedkv.PKV_MAX_SPLITS
+
+
+def test_auto_path_is_a_kernel_family():
+    assert pagedkv.path_for(base_desc()) in (pagedkv.PKV_PATH_VALU, pagedkv.PKV_PATH_MFMA)
+    assert pagedkv.path_for(base_desc(path=pagedkv.PKV_PATH_VALU)) == pagedkv.PKV_PATH_VALU
+
+
+def test_run_kernel_rejects_unsupported_modes_without_launching():
+    lib = _lib.load()
+    p = ctypes.c_void_p(4096)
+    lib.run_kernel(p, p, p, p, p, p, 4, 128, 2, 32, 8, 128, 16, 64, 0)   # seqlen_q = 2
+    assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
+    lib.run_kernel(p, p, p, p, p, p, 4, 128, 1, 32, 8, 128, 16, 64, 1)   # causal
+    assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
+    lib.run_kernel(p, p, p, p, p, p, 4, 128, 1, 32, 8, 96, 16, 64, 0)    # head_dim 96
+    assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
