@@ -95,10 +95,11 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k, head_dim=D,
         page_size=cfg.page_size, num_pages=base["k_cache"].shape[0], block_table_stride=cfg.block_table.shape[1],
         dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
-        max_seqlen=int(cfg.seqlens.max()), path=args.path,
+        max_seqlen=int(cfg.seqlens.max()), path=args.path, split_tokens=args.split_tokens,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
+    split_tokens = pagedkv.split_tokens_for(desc, splits_req)
     path = pagedkv.path_for(desc)
     ws_bytes = pagedkv.workspace_size(desc, splits_req)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
@@ -158,6 +159,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         "partition_us": part_avg_ms * 1e3,
         "combine_us": sum(comb_ms) / K * 1e3,
         "splits": splits,
+        "split_tokens": split_tokens,
         "path": {1: "valu", 2: "mfma"}.get(path, str(path)),
         "roofline": {
             "bound": "hbm",
@@ -216,10 +218,14 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=3, help="independent KV pools rotated across calls")
     ap.add_argument("--path", type=int, default=0, help="0 auto, 1 VALU, 2 MFMA")
     ap.add_argument("--splits", type=int, default=None, help="num_splits (default: the config's, 0 = heuristic)")
+    ap.add_argument("--split-tokens", type=int, default=0, help="token window per split when num_splits is 0")
     ap.add_argument("--all", action="store_true", help="also measure every other config (extra lines to --json-out)")
     ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of benchmarking, run a plain device copy of MIB MiB (read + write) five times; "
+                         "used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -234,6 +240,15 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1.0, out=dst)  # one elementwise launch: reads n*4 bytes, writes n*4 bytes
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_read": n * 4, "calibrate_copy_bytes_written": n * 4}), flush=True)
+        return 0
     events = HipEvents()
     names = [args.config] + ([n for n in ("c1", "c2", "c3", "c4", "c5") if n != args.config] if args.all else [])
     lines = []
@@ -254,7 +269,8 @@ def main() -> int:
             "vs_baseline": None,
             "dtype": cfg.dtype,
             "data": "synthetic (seeded N(0,1) values, random paged layout; see pagedkv/configs.py)",
-            "config": {**cfg.describe(), "splits": res["splits"], "path": res["path"], "kv_sets": args.sets},
+            "config": {**cfg.describe(), "splits": res["splits"], "split_tokens": res["split_tokens"],
+                       "path": res["path"], "kv_sets": args.sets},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
             "hbm_frac_kv": round(res["kv_gbps"] / HBM_PEAK_GBPS, 4),
@@ -273,7 +289,7 @@ def main() -> int:
         print(f"[bench] {name}: {line['us_per_call']} us/call, {line['value']} GB/s KV "
               f"({100 * line['hbm_frac_kv']:.1f}% of peak), partition {line['partition_us']} us "
               f"({100 * line['roofline']['frac']:.1f}% roofline), combine {line['combine_us']} us, "
-              f"splits {res['splits']}, path {res['path']}", file=sys.stderr, flush=True)
+              f"splits {res['splits']} (window {res['split_tokens']}), path {res['path']}", file=sys.stderr, flush=True)
         del res
         torch.cuda.empty_cache()
     if args.json_out:

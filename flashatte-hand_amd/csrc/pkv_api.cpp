@@ -21,12 +21,12 @@ namespace {
 
 // gfx950 (MI355X) compute units; the split heuristic sizes grids against it.
 constexpr int kComputeUnits = 256;
-// Work items (waves) per CU the heuristic aims for: enough independent
-// 16-byte/lane streams in flight to cover HBM latency.
-constexpr int kTargetWavesPerCU = 16;
-// Shortest split worth a separate partial (tokens): below this the partial
-// O write + combine read outweigh the extra parallelism.
-constexpr int kMinTokensPerSplit = 256;
+// Resident waves per CU the heuristic assumes for the partition kernel.
+constexpr int kWavesPerCU = 12;
+// Split windows are at least this long: shorter ones spend more on the item
+// prologue, the partial write and the combine than they gain in parallelism.
+constexpr int kMinSplitTokens = 256;
+constexpr int kMaxSplitTokens = 8192;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
@@ -86,6 +86,9 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (d->path != PKV_PATH_AUTO && d->path != PKV_PATH_VALU && d->path != PKV_PATH_MFMA) {
         return PKV_EINVAL;
     }
+    if (d->split_tokens < 0 || d->split_tokens % 16 != 0 || d->reserved != 0) {
+        return PKV_EINVAL;
+    }
     // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.
     if (d->batch * d->num_heads > (int64_t{1} << 30) || d->num_pages > INT32_MAX ||
         d->block_table_stride > INT32_MAX) {
@@ -107,32 +110,57 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     return PKV_OK;
 }
 
-// Split count: aim for kTargetWavesPerCU waves per CU across the whole grid,
-// but never below kMinTokensPerSplit tokens per split of the longest row and
-// never more splits than that row has pages (or PKV_MAX_SPLITS).  Unlike the
-// reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
-// it counts KV heads, head groups and the CU count of the part.
-int choose_splits(const Resolved& r, int64_t max_seqlen) {
-    const int64_t items = r.B * r.Hk * r.head_groups;
-    const int64_t target = int64_t{kComputeUnits} * kTargetWavesPerCU;
-    int64_t s = (target + items - 1) / items;
-    const int64_t by_len = std::max<int64_t>(1, max_seqlen / kMinTokensPerSplit);
-    s = std::min(s, by_len);
-    s = std::min<int64_t>(s, r.max_pages);
-    s = std::min<int64_t>(s, PKV_MAX_SPLITS);
-    return static_cast<int>(std::max<int64_t>(1, s));
+// How the rows are cut into splits for one call.
+struct SplitPlan {
+    int splits;       // split slots per (b, h) row (0 = invalid request)
+    int split_tokens; // > 0: fixed token windows; 0: page-balanced splits
+};
+
+int64_t effective_max_seqlen(const pkv_decode_desc* d, const Resolved& r) {
+    const int64_t row_cap = d->block_table_stride * r.P;
+    return d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
 }
 
-int resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
-    if (num_splits < 0) {
-        return 0;
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Window length for the heuristic: about two work items per resident wave
+// slot of the 256 CUs, assuming rows average half of max_seqlen, clamped to
+// [kMinSplitTokens, kMaxSplitTokens] and rounded to a power of two.  Unlike the
+// reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
+// it counts KV heads, head groups and the CU count, and equal windows keep
+// ragged rows from leaving a long tail of oversized items.
+int64_t choose_split_tokens(const Resolved& r, int64_t max_seqlen) {
+    const int64_t units = r.B * r.Hk * r.head_groups;
+    const int64_t slots = int64_t{kComputeUnits} * kWavesPerCU;
+    const int64_t est_tokens = units * std::max<int64_t>(1, max_seqlen / 2);
+    const int64_t want = est_tokens / (2 * slots);
+    int64_t tok = kMinSplitTokens;
+    while (tok < want && tok < kMaxSplitTokens) {
+        tok *= 2;
     }
-    const int64_t row_cap = d->block_table_stride * r.P;
-    const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
-    int64_t s = num_splits == 0 ? choose_splits(r, max_seqlen) : num_splits;
-    s = std::min<int64_t>(s, r.max_pages);
+    return tok;
+}
+
+SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
+    if (num_splits < 0) {
+        return {0, 0};
+    }
+    const int64_t max_seqlen = effective_max_seqlen(d, r);
+    if (num_splits == 0) {
+        int64_t tok = d->split_tokens > 0 ? d->split_tokens : choose_split_tokens(r, max_seqlen);
+        int64_t s = (max_seqlen + tok - 1) / tok;
+        if (s > PKV_MAX_SPLITS) {
+            tok = round_up((max_seqlen + PKV_MAX_SPLITS - 1) / PKV_MAX_SPLITS, 16);
+            s = (max_seqlen + tok - 1) / tok;
+        }
+        if (s <= 1) {
+            return {1, 0};
+        }
+        return {static_cast<int>(s), static_cast<int>(tok)};
+    }
+    int64_t s = std::min<int64_t>(num_splits, r.max_pages);
     s = std::min<int64_t>(s, PKV_MAX_SPLITS);
-    return static_cast<int>(std::max<int64_t>(1, s));
+    return {static_cast<int>(std::max<int64_t>(1, s)), 0};
 }
 
 constexpr size_t kAlign = 256;
@@ -177,7 +205,15 @@ int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    return resolve_splits(desc, r, num_splits);
+    return resolve_splits(desc, r, num_splits).splits;
+}
+
+int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits).split_tokens;
 }
 
 int pkv_decode_path(const pkv_decode_desc* desc) {
@@ -193,8 +229,8 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    const int splits = resolve_splits(desc, r, num_splits);
-    return workspace_bytes(r, splits);
+    const SplitPlan plan = resolve_splits(desc, r, num_splits);
+    return workspace_bytes(r, plan.splits);
 }
 
 int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
@@ -215,7 +251,8 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     if (num_splits < 0 || !std::isfinite(softmax_scale)) {
         return PKV_EINVAL;
     }
-    const int splits = resolve_splits(desc, r, num_splits);
+    const SplitPlan plan = resolve_splits(desc, r, num_splits);
+    const int splits = plan.splits;
     const size_t need = workspace_bytes(r, splits);
     if (need > 0 && (desc->workspace == nullptr || desc->workspace_bytes < need || !aligned16(desc->workspace))) {
         return PKV_ENOWORKSPACE;
@@ -244,11 +281,23 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     p.group = static_cast<int32_t>(r.group);
     p.head_groups = r.head_groups;
     p.splits = splits;
+    p.split_tokens = plan.split_tokens;
     p.page_shift = r.page_shift;
     p.bt_stride = static_cast<int32_t>(desc->block_table_stride);
     p.num_pages = static_cast<int32_t>(desc->num_pages);
     p.row_cap = static_cast<int32_t>(std::min<int64_t>(desc->block_table_stride * r.P, INT32_MAX));
+    p.batch = static_cast<int32_t>(r.B);
     p.num_items = static_cast<int32_t>(items);
+    // With strided wave->item mapping, a multiple of 8 workgroups so each XCD
+    // owns the items with index = XCD mod 8 (see decode_item).
+    {
+        const int64_t groups = (items + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup;
+        p.num_groups = static_cast<int32_t>(PKV_STRIDED_ITEMS ? round_up(groups, 8) : groups);
+    }
+#ifndef PKV_ITEM_ORDER
+#define PKV_ITEM_ORDER 1
+#endif
+    p.split_fastest = PKV_ITEM_ORDER == 1 ? 0 : PKV_ITEM_ORDER == 2 ? 1 : ((r.Hk * r.head_groups) % 8 == 0 ? 0 : 1);
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
@@ -271,9 +320,14 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         pkv::CombineParams c{};
         c.part_o = p.part_o;
         c.part_lse = p.part_lse;
+        c.seqlens = cache_seqlens;
         c.out = p.out;
         c.rows = static_cast<int32_t>(r.B * r.H);
+        c.num_heads = static_cast<int32_t>(r.H);
         c.splits = splits;
+        c.split_tokens = plan.split_tokens;
+        c.page_shift = r.page_shift;
+        c.row_cap = p.row_cap;
         if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s) != hipSuccess) {
             return PKV_ELAUNCH;
         }

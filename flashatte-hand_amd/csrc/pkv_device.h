@@ -27,21 +27,31 @@ struct PartitionParams {
     int32_t num_heads_k;  // Hk
     int32_t group;        // H / Hk
     int32_t head_groups;  // ceil(group / heads per wave)
-    int32_t splits;
+    int32_t splits;       // split slots per (b, h) row
+    int32_t split_tokens; // > 0: split s covers tokens [s*split_tokens, (s+1)*split_tokens);
+                          // 0: page-balanced splits of each row (the reference's scheme)
     int32_t page_shift;   // log2(P)
     int32_t bt_stride;
     int32_t num_pages;
     int32_t row_cap;      // tokens a block_table row can address (bt_stride * P, clamped)
-    int32_t num_items;    // B * Hk * head_groups * splits
+    int32_t batch;        // B
+    int32_t num_items;    // splits * B * Hk * head_groups
+    int32_t num_groups;   // workgroups in the grid (a multiple of 8)
+    int32_t split_fastest; // item order: 1 = split index fastest, 0 = (kv head, head group) fastest
     float scale_log2;     // softmax_scale * log2(e)
 };
 
 struct CombineParams {
     const float* part_o;
     const float* part_lse;
+    const int32_t* seqlens;
     uint16_t* out;
-    int32_t rows;   // B * H
+    int32_t rows;         // B * H
+    int32_t num_heads;    // H
     int32_t splits;
+    int32_t split_tokens; // as in PartitionParams
+    int32_t page_shift;
+    int32_t row_cap;
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -96,6 +106,22 @@ __device__ __forceinline__ uint16_t from_f32(float f) {
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
     return static_cast<uint32_t>(from_f32<BF16>(a)) | (static_cast<uint32_t>(from_f32<BF16>(b)) << 16);
+}
+
+// Two fp32 -> packed 16-bit with the hardware pack (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32, round to nearest even).  Used for the softmax
+// probabilities fed to MFMA; outputs use the explicit conversions above.
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2_hw(float a, float b) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t v = {a, b};
+    if constexpr (BF16) {
+        typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    } else {
+        typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+    }
 }
 
 // ---------------------------------------------------------------- loads
@@ -166,6 +192,28 @@ __device__ __forceinline__ float group_max(float x) {
     return x;
 }
 
+// Reductions across the four 16-lane rows of a wave with the gfx950 row-swap
+// instructions (VALU only, no LDS round trip).  permlane16_swap(x, x) returns
+// (even-row copy, odd-row copy) of each row pair, permlane32_swap(x, x) the
+// (low-half, high-half) copies, so op(first, second) is the pair reduction on
+// every lane, with bit-identical results on both partners.
+__device__ __forceinline__ float max_rows16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_rows16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_halves32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Exchange with the lane `STRIDE` away (STRIDE in {8, 16, 32}) — used to merge
 // the per-row online-softmax states of a wave.
 template <int STRIDE>
@@ -179,25 +227,95 @@ __device__ __forceinline__ float xor_lane(float x) {
 
 // ---------------------------------------------------------------- indexing
 
-// Split s of S covers pages [n*s/S, n*(s+1)/S) of the row's n valid pages
-// (best_flashattn_kvcache_decode.cu:664-671): any two splits differ by at most one page.
+// Token range of split `split` of a row with `seqlen` valid tokens.
+// split_tokens > 0: fixed windows of split_tokens tokens, so every work item
+// streams the same amount and ragged rows simply own fewer items.
+// split_tokens == 0: split s covers pages [n*s/S, n*(s+1)/S) of the row's n
+// valid pages (best_flashattn_kvcache_decode.cu:664-671), so any two splits of
+// a row differ by at most one page.  Either way the range may be empty.
 struct TokenRange {
     int32_t begin;
     int32_t end;
 };
 
-__device__ __forceinline__ TokenRange split_tokens(int32_t seqlen, int32_t page_shift, int32_t split,
-                                                   int32_t splits) {
+__device__ __forceinline__ TokenRange split_tokens_of(int32_t seqlen, int32_t page_shift, int32_t split,
+                                                      int32_t splits, int32_t split_tokens) {
+    TokenRange r;
+    if (split_tokens > 0) {
+        r.begin = split * split_tokens;
+        r.end = max(r.begin, min(r.begin + split_tokens, seqlen));
+        return r;
+    }
     const int32_t pages = seqlen > 0 ? ((seqlen - 1) >> page_shift) + 1 : 0;
     const int32_t first = static_cast<int32_t>((static_cast<int64_t>(pages) * split) / splits);
     const int32_t last = static_cast<int32_t>((static_cast<int64_t>(pages) * (split + 1)) / splits);
-    TokenRange r;
     r.begin = first << page_shift;
-    r.end = min(last << page_shift, seqlen);
-    if (first >= last) {
-        r.end = r.begin; // empty split
-    }
+    r.end = first < last ? min(last << page_shift, seqlen) : r.begin;
     return r;
+}
+
+// Work items and the 8 XCDs.  Workgroups are dealt to the XCDs round-robin
+// (workgroup w runs on XCD w % 8), so wave k of workgroup w takes item
+// k * num_groups + w: with num_groups a multiple of 8, XCD x owns exactly the
+// items whose index is x mod 8.  The item index puts a dimension that every
+// row has equally many of fastest — the (kv head, head group) unit when there
+// are a multiple of 8 of them, else the split window — so each XCD gets the
+// same share of every row and ragged rows cannot overload one XCD.
+struct Item {
+    int32_t split;
+    int32_t b;
+    int32_t kvh;
+    int32_t hg;
+};
+
+#ifndef PKV_WAVES_PER_GROUP
+#define PKV_WAVES_PER_GROUP 4
+#endif
+#ifndef PKV_STRIDED_ITEMS
+#define PKV_STRIDED_ITEMS 0
+#endif
+constexpr int kWavesPerGroup = PKV_WAVES_PER_GROUP;
+
+__device__ __forceinline__ int32_t wave_item(const PartitionParams& p) {
+    const int32_t wave = static_cast<int32_t>(threadIdx.x >> 6);
+    if (PKV_STRIDED_ITEMS) {
+        return wave * p.num_groups + static_cast<int32_t>(blockIdx.x);
+    }
+    return static_cast<int32_t>(blockIdx.x) * kWavesPerGroup + wave;
+}
+
+__device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams& p) {
+    const int32_t units = p.num_heads_k * p.head_groups;
+    Item it;
+    int32_t u;
+    if (p.split_fastest) {
+        it.split = item % p.splits;
+        const int32_t rest = item / p.splits;
+        u = rest % units;
+        it.b = rest / units;
+    } else {
+        u = item % units;
+        const int32_t rest = item / units;
+        it.b = rest % p.batch;
+        it.split = rest / p.batch;
+    }
+    it.kvh = u / p.head_groups;
+    it.hg = u - it.kvh * p.head_groups;
+    return it;
+}
+
+// Page-id window: lane l holds the physical id of logical page base + l of the
+// row (64 pages per window).  Kernels read ids from it with readlane /
+// ds_bpermute, so the K/V address of a tile never waits on a global load —
+// a dependent global load would force the wave to drain (vmcnt is in order)
+// every K/V load it has in flight.  Out-of-range ids are clamped to page 0 so a
+// corrupt table cannot fault the GPU; entries past the row's last page are 0
+// and never used.
+__device__ __forceinline__ int32_t load_page_window(const int32_t* __restrict__ bt_row, int32_t base,
+                                                    int32_t last_page, int32_t lane, int32_t num_pages) {
+    const int32_t idx = base + lane;
+    const int32_t v = idx <= last_page ? bt_row[idx] : 0;
+    return static_cast<uint32_t>(v) < static_cast<uint32_t>(num_pages) ? v : 0;
 }
 
 // Element offset of (token t, kv head base) given the row's block_table.

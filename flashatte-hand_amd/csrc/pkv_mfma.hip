@@ -15,9 +15,9 @@
 //   O^T[D x 16 heads] += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
 //       v_mfma_f32_16x16x16{bf16_1k,f16}, D/16 output tiles.  A = V^T needs
 //       4 tokens of one dim per lane, so the V tile (loaded with the same
-//       addresses as K) is written to a per-wave LDS tile whose 16-byte chunks
-//       are XOR-swizzled by token (chunk c of token t sits at c ^ t), which
-//       keeps both the row writes and the column gathers free of bank conflicts.
+//       addresses as K) is written to a per-wave LDS tile with rows padded by
+//       16 bytes, which spreads both the row writes and the column gathers
+//       over distinct banks.
 //   The next tile's K and V are loaded into a second register set before the
 //   current tile is computed.
 // The per-wave LDS tile is private to the wave and LDS operations of a wave
@@ -68,103 +68,235 @@ struct TileRegs {
     uint4 v[D / 32];
 };
 
-template <int D>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams& p, const int32_t* __restrict__ bt_row,
-                                          int t0, int end, int n, int64_t lane_off) {
-    const int t = min(t0 + n, end - 1); // clamp: never touch unowned slots
-    const int64_t off = token_elem_offset(bt_row, t, p) + lane_off;
+// Issue the K and V loads of the 16-token tile starting at t0 in row layout:
+// the L = D/8 lanes of a row read one token's D contiguous 16-bit values of
+// this KV head (whole 128-byte lines), so one instruction covers R = 64/L
+// tokens and a tile takes D/32 instructions per tensor.  (Reading the MFMA
+// operand layout straight from HBM — 16 tokens x 64 bytes per instruction —
+// streams measurably slower, so K is re-laid out through LDS instead.)
+// WIDE: P >= 16, so the tile lies inside one page whose id is wave-uniform and
+// is read from the page window with readlane; otherwise each lane fetches its
+// own token's page id from the window with ds_bpermute.  Neither waits on a
+// global load, so earlier tiles' loads stay in flight.  When `real` is false
+// (a prefetch past the end of the range) every lane loads the same 16 bytes at
+// the start of the caches instead: the loop then issues the same number of
+// loads on every path, which keeps the compiler's wait counts exact.
+template <int D, bool WIDE>
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams& p, int win, int win_base, int t0,
+                                          int end, bool real, int lane, int kvh) {
+    constexpr int L = D / 8;
+    constexpr int R = 64 / L;
+    constexpr int NI = D / 32;
+    const int rl = lane / L;
+    const int lane_off = kvh * D + 8 * (lane % L);
+    const int pmask = (1 << p.page_shift) - 1;
+    if constexpr (WIDE) {
+        const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
+        const int phys = __builtin_amdgcn_readlane(win, idx);
+        const int64_t base = real ? static_cast<int64_t>(phys) * p.page_stride : 0;
+        const uint16_t* kb = p.k + base;
+        const uint16_t* vb = p.v + base;
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) {
-        r.k[kk] = load_kv16(p.k + off + 32 * kk);
-        r.v[kk] = load_kv16(p.v + off + 32 * kk);
+        for (int i = 0; i < NI; ++i) {
+            const int t = min(t0 + R * i + rl, end - 1); // clamp: never touch unowned slots
+            const int off = real ? (t & pmask) * static_cast<int>(p.token_stride) + lane_off : 0;
+            r.k[i] = load_kv16(kb + off);
+            r.v[i] = load_kv16(vb + off);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = min(t0 + R * i + rl, end - 1);
+            const int phys = __shfl(win, real ? (t >> p.page_shift) - win_base : 0, 64);
+            const int64_t off = real ? static_cast<int64_t>(phys) * p.page_stride +
+                                           static_cast<int64_t>((t & pmask) * static_cast<int>(p.token_stride) +
+                                                                lane_off)
+                                     : 0;
+            r.k[i] = load_kv16(p.k + off);
+            r.v[i] = load_kv16(p.v + off);
+        }
     }
 }
 
+// LDS tiles of one wave: 16 token rows of K and of V, each row padded by 16
+// bytes (row stride 2D + 16 bytes).  The padding shifts consecutive rows by 16
+// bytes across the banks, so the row writes, the K operand reads (16 rows,
+// same chunk) and the V column gathers (4 rows x 32 contiguous bytes) are
+// spread over distinct banks, and every address is a per-lane base plus an
+// immediate offset.
+template <int D>
+struct VTile {
+    static constexpr int kRow = D + 8; // row stride in 16-bit elements
+    static constexpr int kElems = 16 * kRow;
+};
+
+// Part 1 of a tile: stage the K and V rows in the wave's LDS tiles, read K back
+// in MFMA A-operand layout (lane (n, j): token n, dims 8(4kk + j) .. +7) and
+// compute S^T = K Q^T.  After this the tile's registers are free for the next
+// prefetch.
 template <bool BF16, int D>
-__device__ __forceinline__ void process_tile(const TileRegs<D>& r, const uint4 (&qop)[D / 32], f32x4 (&o)[D / 16],
-                                             float& m, float& l, uint16_t* lds, int t0, int end, int n, int j,
-                                             float scale_log2) {
-    constexpr int KS = D / 32;
-    constexpr int DT = D / 16;
-    constexpr int CHM = D / 8 - 1; // 16-byte chunks per token row, minus one
-
-    // V tile -> LDS, row n, logical chunk 4kk + j stored at chunk (4kk + j) ^ n.
+__device__ __forceinline__ f32x4 tile_scores(const TileRegs<D>& r, const uint4 (&qop)[D / 32], uint16_t* lds, int lane,
+                                             int n, int j) {
+    constexpr int L = D / 8;
+    constexpr int R = 64 / L;
+    constexpr int NI = D / 32;
+    uint16_t* kt = lds;
+    uint16_t* vt = lds + VTile<D>::kElems;
+    const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-        *reinterpret_cast<uint4*>(lds + n * D + 8 * ((4 * kk + j) ^ (n & CHM))) = r.v[kk];
+    for (int i = 0; i < NI; ++i) {
+        *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
+        *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
     }
-
+    uint4 ka[D / 32];
+    const uint16_t* kr = kt + n * VTile<D>::kRow + 8 * j;
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+        ka[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
+    }
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-        s = mfma_qk<BF16>(r.k[kk], qop[kk], s);
+    for (int kk = 0; kk < D / 32; ++kk) {
+        s = mfma_qk<BF16>(ka[kk], qop[kk], s);
     }
+    return s;
+}
 
+// Rescale threshold of the running max (log2 units): probabilities are taken
+// relative to a reference max m that is only raised when a tile's max exceeds
+// it by more than this, so p <= 2^8 (exact in fp16/bf16 range) and the
+// accumulator rescale runs only a handful of times per item.  The result is
+// the same softmax: numerator and denominator share the reference.
+constexpr float kLazyRescaleLog2 = 8.0f;
+
+// Part 2 of a tile: mask, online softmax (fp32, log2 domain), P pack and
+// O^T += V^T P^T on MFMA with V^T gathered from the LDS tile.
+template <bool BF16, int D>
+__device__ __forceinline__ void tile_softmax_pv(const f32x4& s, f32x4 (&o)[D / 16], float& m, float& l,
+                                                const uint16_t* lds, int t0, int end, int n, int j,
+                                                float scale_log2) {
+    constexpr int DT = D / 16;
     float sc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         sc[i] = (t0 + 4 * j + i) < end ? s[i] * scale_log2 : kNegInf;
     }
     float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tmax = fmaxf(tmax, swizzle_xor_f32<16>(tmax));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
-    m = m_new;
-    if (__any(alpha != 1.f)) {
+    tmax = max_halves32(max_rows16(tmax));
+    if (__any(tmax > m + kLazyRescaleLog2)) {
+        const float m_new = tmax > m + kLazyRescaleLog2 ? tmax : m;
+        const float alpha = fast_exp2(m - m_new); // 0 on the first tile (m = -inf), 1 if unchanged
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             o[dt] *= alpha;
         }
+        l *= alpha;
+        m = m_new;
     }
     float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        pr[i] = fast_exp2(sc[i] - m_use);
+        pr[i] = fast_exp2(sc[i] - m);
     }
-    l = l * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
     uint2 pb;
-    pb.x = pack2<BF16>(pr[0], pr[1]);
-    pb.y = pack2<BF16>(pr[2], pr[3]);
+    pb.x = pack2_hw<BF16>(pr[0], pr[1]);
+    pb.y = pack2_hw<BF16>(pr[2], pr[3]);
 
-    // O^T tile dt: A = V^T, lane gathers V[4j + i][16 dt + n] for i = 0..3.
+    // O^T tile dt: A = V^T needs V[4j + i][16 dt + n] (i = 0..3) in lane (n, j).
+    // ds_read_b64_tr_b16 hands lane i of each 16-lane row the elements
+    // M[i / 4 + 4e][i % 4] (e = 0..3) of the 4-element chunks M[r] its row's
+    // lanes address, so lane (n, j) addresses V[4j + n / 4][16 dt + 4 (n % 4)].
+    typedef short s16x4_t __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+    const uint16_t* rd = lds + VTile<D>::kElems + (4 * j + (n >> 2)) * VTile<D>::kRow + 4 * (n & 3);
+    uint2 a[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-        const int c = 2 * dt + (n >> 3);
-        const int e = n & 7;
-        uint16_t x[4];
+        const s16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)((__attribute__((address_space(3))) uint16_t*)(rd + 16 * dt)));
+        a[dt] = __builtin_bit_cast(uint2, t);
+    }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tok = 4 * j + i;
-            x[i] = lds[tok * D + 8 * (c ^ (tok & CHM)) + e];
-        }
-        uint2 a;
-        a.x = static_cast<uint32_t>(x[0]) | (static_cast<uint32_t>(x[1]) << 16);
-        a.y = static_cast<uint32_t>(x[2]) | (static_cast<uint32_t>(x[3]) << 16);
-        o[dt] = mfma_pv<BF16>(a, pb, o[dt]);
+    for (int dt = 0; dt < DT; ++dt) {
+        o[dt] = mfma_pv<BF16>(a[dt], pb, o[dt]);
     }
 }
 
-template <bool BF16, int D>
-__global__ __launch_bounds__(256) void partition_mfma_kernel(PartitionParams p) {
+// Walks the tiles of [t, end) with DEPTH tiles of loads in flight.  RELOAD
+// adds the page-window refresh for ranges longer than 64 pages (a dependent
+// global load, so it drains the pipeline once per 64 pages); the common path
+// has none and every prefetch is unconditional, so all waits are exact.
+template <bool BF16, int D, bool WIDE, int DEPTH, bool RELOAD>
+__device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_t* __restrict__ bt_row, int last_page,
+                                          int& win, int& win_base, const uint4 (&qop)[D / 32], f32x4 (&o)[D / 16],
+                                          float& m, float& l, uint16_t* lds, int t, int end, int lane, int n,
+                                          int j, int kvh) {
+    auto ensure_window = [&](int tn) {
+        if constexpr (RELOAD) {
+            const int tl = min(tn + 15, end - 1);
+            if (tn < end && (tl >> p.page_shift) - win_base >= 64) {
+                win_base = tn >> p.page_shift;
+                win = load_page_window(bt_row, win_base, last_page, threadIdx.x & 63, p.num_pages);
+            }
+        }
+    };
+    // Counted loops without a mid-body exit: a `break` between the two halves
+    // would be structurized through the loop header and make the compiler's
+    // wait counts assume the just-issued prefetch is the tile being consumed.
+    const int ntiles = (end - t + 15) >> 4;
+    TileRegs<D> ra;
+    load_tile<D, WIDE>(ra, p, win, win_base, t, end, true, lane, kvh);
+    if constexpr (DEPTH == 1) {
+        for (int k = 0; k < ntiles; ++k) {
+            const f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            ensure_window(t + 16);
+            load_tile<D, WIDE>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
+            tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
+            t += 16;
+        }
+    } else {
+        TileRegs<D> rb;
+        ensure_window(t + 16);
+        load_tile<D, WIDE>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
+        for (int k = 0; k + 2 <= ntiles; k += 2) {
+            f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            ensure_window(t + 32);
+            load_tile<D, WIDE>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
+            tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
+            t += 16;
+            s = tile_scores<BF16, D>(rb, qop, lds, lane, n, j);
+            ensure_window(t + 32);
+            load_tile<D, WIDE>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
+            tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
+            t += 16;
+        }
+        if (ntiles & 1) {
+            const f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
+        }
+    }
+}
+
+template <bool BF16, int D, bool WIDE, int DEPTH>
+__global__ __launch_bounds__(64 * kWavesPerGroup) void partition_mfma_kernel(PartitionParams p) {
     constexpr int KS = D / 32;
     constexpr int DT = D / 16;
-    constexpr int kWaves = 4;
-    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][16 * D];
+    constexpr int kWaves = kWavesPerGroup;
+    static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
+    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][2 * VTile<D>::kElems];
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * kWaves + wave;
+    const int item = wave_item(p);
     if (item >= p.num_items) {
         return;
     }
-    const int split = item % p.splits;
-    int rest = item / p.splits;
-    const int hg = rest % p.head_groups;
-    rest /= p.head_groups;
-    const int kvh = rest % p.num_heads_k;
-    const int b = rest / p.num_heads_k;
+    const Item it = decode_item(item, p);
+    const int split = it.split;
+    const int b = it.b;
+    const int kvh = it.kvh;
+    const int hg = it.hg;
 
     const int n = lane & 15;
     const int j = lane >> 4;
@@ -173,29 +305,28 @@ __global__ __launch_bounds__(256) void partition_mfma_kernel(PartitionParams p) 
     const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
 
     const int seqlen = min(p.seqlens[b], p.row_cap);
-    const TokenRange range = split_tokens(seqlen, p.page_shift, split, p.splits);
+    const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
 
     if (range.begin >= range.end) {
-        constexpr int CH = D / 8; // 16-byte output chunks per head
-        for (int idx = lane; idx < heads_here * CH; idx += 64) {
-            const int g = idx / CH;
-            const int c = idx % CH;
-            if (p.splits == 1) {
-                uint4 z = {0u, 0u, 0u, 0u};
-                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + c * 8) = z;
-            } else {
-                const int64_t pi = (bh_first + g) * p.splits + split;
-                float4 z = {0.f, 0.f, 0.f, 0.f};
-                float4* dst = reinterpret_cast<float4*>(p.part_o + pi * D + c * 8);
-                dst[0] = z;
-                dst[1] = z;
+        // Empty range.  With one split the row has no tokens: its output is 0.
+        // With several, the combine derives each row's non-empty splits from
+        // cache_seqlens and never reads this item's slot, so nothing is written.
+        if (p.splits == 1) {
+            constexpr int CH = D / 8; // 16-byte output chunks per head
+            for (int idx = lane; idx < heads_here * CH; idx += 64) {
+                const int g = idx / CH;
+                const int c = idx % CH;
+                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + c * 8) = make_uint4(0u, 0u, 0u, 0u);
             }
-        }
-        if (p.splits > 1 && lane < heads_here) {
-            p.part_lse[(bh_first + lane) * p.splits + split] = kNegInf;
         }
         return;
     }
+
+    const int end = range.end;
+    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+    const int last_page = (end - 1) >> p.page_shift;
+    int win_base = range.begin >> p.page_shift;
+    int win = load_page_window(bt_row, win_base, last_page, lane, p.num_pages);
 
     // B operand of QK: head n, dims 8(4kk + j) .. +7; zero columns past the group.
     uint4 qop[KS];
@@ -216,36 +347,19 @@ __global__ __launch_bounds__(256) void partition_mfma_kernel(PartitionParams p) 
     float m = kNegInf;
     float l = 0.f;
 
-    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-    const int64_t lane_off = static_cast<int64_t>(kvh) * D + 8 * j;
     uint16_t* lds = lds_tiles[wave];
-    const int end = range.end;
 
-    TileRegs<D> ra, rb;
-    int t = range.begin;
-    load_tile<D>(ra, p, bt_row, t, end, n, lane_off);
-    while (true) {
-        if (t + 16 < end) {
-            load_tile<D>(rb, p, bt_row, t + 16, end, n, lane_off);
-        }
-        process_tile<BF16, D>(ra, qop, o, m, l, lds, t, end, n, j, p.scale_log2);
-        t += 16;
-        if (t >= end) {
-            break;
-        }
-        if (t + 16 < end) {
-            load_tile<D>(ra, p, bt_row, t + 16, end, n, lane_off);
-        }
-        process_tile<BF16, D>(rb, qop, o, m, l, lds, t, end, n, j, p.scale_log2);
-        t += 16;
-        if (t >= end) {
-            break;
-        }
+    if (last_page - win_base < 64) {
+        // Common case: the whole range fits in one page window.
+        tile_loop<BF16, D, WIDE, DEPTH, false>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, range.begin,
+                                               end, lane, n, j, kvh);
+    } else {
+        tile_loop<BF16, D, WIDE, DEPTH, true>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, range.begin,
+                                              end, lane, n, j, kvh);
     }
 
     // l holds this lane's 4-token partial sums; total over the 4 lanes of head n.
-    l += swizzle_xor_f32<16>(l);
-    l += __shfl_xor(l, 32, 64);
+    l = sum_halves32(sum_rows16(l));
 
     if (n >= heads_here) {
         return;
@@ -275,11 +389,21 @@ __global__ __launch_bounds__(256) void partition_mfma_kernel(PartitionParams p) 
     }
 }
 
+#ifndef PKV_MFMA_DEPTH
+#define PKV_MFMA_DEPTH 2
+#endif
+
 template <bool BF16, int D>
 static hipError_t launch_mfma_t(const PartitionParams& p, hipStream_t stream) {
-    constexpr int kWaves = 4;
-    const int blocks = (p.num_items + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL((partition_mfma_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    constexpr int kWaves = kWavesPerGroup;
+    const int blocks = p.num_groups;
+    if (p.page_shift >= 4) {
+        hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves), 0,
+                           stream, p);
+    } else {
+        hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves),
+                           0, stream, p);
+    }
     return hipGetLastError();
 }
 

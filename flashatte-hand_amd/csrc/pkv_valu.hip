@@ -22,22 +22,21 @@
 namespace pkv {
 
 template <bool BF16, int D, int GT, int NT>
-__global__ __launch_bounds__(256) void partition_valu_kernel(PartitionParams p) {
+__global__ __launch_bounds__(64 * kWavesPerGroup) void partition_valu_kernel(PartitionParams p) {
     constexpr int L = D / 8;   // lanes per token row
     constexpr int R = 64 / L;  // token rows per wave
     static_assert(L * R == 64, "head_dim must be 64, 128, 256 or 512");
 
     const int lane = threadIdx.x & 63;
-    const int item = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int item = wave_item(p);
     if (item >= p.num_items) {
         return;
     }
-    const int split = item % p.splits;
-    int rest = item / p.splits;
-    const int hg = rest % p.head_groups;
-    rest /= p.head_groups;
-    const int kvh = rest % p.num_heads_k;
-    const int b = rest / p.num_heads_k;
+    const Item it = decode_item(item, p);
+    const int split = it.split;
+    const int b = it.b;
+    const int kvh = it.kvh;
+    const int hg = it.hg;
 
     const int row = lane / L;
     const int sub = lane % L;
@@ -47,23 +46,14 @@ __global__ __launch_bounds__(256) void partition_valu_kernel(PartitionParams p) 
     const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + h_first;
 
     const int seqlen = min(p.seqlens[b], p.row_cap);
-    const TokenRange range = split_tokens(seqlen, p.page_shift, split, p.splits);
+    const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
 
     if (range.begin >= range.end) {
-        // Empty split (or seqlen <= 0): O = 0 and LSE = -inf, or zeros in the output.
-        for (int g = row; g < heads_here; g += R) {
-            if (p.splits == 1) {
-                uint4 z = {0u, 0u, 0u, 0u};
-                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + sub * 8) = z;
-            } else {
-                const int64_t pi = (bh_first + g) * p.splits + split;
-                float4 z = {0.f, 0.f, 0.f, 0.f};
-                float4* dst = reinterpret_cast<float4*>(p.part_o + pi * D + sub * 8);
-                dst[0] = z;
-                dst[1] = z;
-                if (sub == 0) {
-                    p.part_lse[pi] = kNegInf;
-                }
+        // Empty range: zeros for a row without tokens (one split); with several
+        // splits the combine skips this slot (it derives them from cache_seqlens).
+        if (p.splits == 1) {
+            for (int g = row; g < heads_here; g += R) {
+                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + sub * 8) = make_uint4(0u, 0u, 0u, 0u);
             }
         }
         return;
@@ -214,8 +204,8 @@ __global__ __launch_bounds__(256) void partition_valu_kernel(PartitionParams p) 
 template <bool BF16, int D, int GT>
 static hipError_t launch_valu_t(const PartitionParams& p, hipStream_t stream) {
     constexpr int NT = GT <= 2 ? 8 : (GT <= 4 ? 8 : (GT <= 8 ? 4 : 2));
-    constexpr int kWaves = 4;
-    const int blocks = (p.num_items + kWaves - 1) / kWaves;
+    constexpr int kWaves = kWavesPerGroup;
+    const int blocks = p.num_groups;
     hipLaunchKernelGGL((partition_valu_kernel<BF16, D, GT, NT>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
     return hipGetLastError();
 }

@@ -42,6 +42,7 @@ __all__ = [
     "run_kernel",
     "workspace_size",
     "num_splits_for",
+    "split_tokens_for",
     "path_for",
     "PkvError",
 ]
@@ -74,6 +75,7 @@ def make_desc(
     dtype: int,
     max_seqlen: int = 0,
     path: int = PKV_PATH_AUTO,
+    split_tokens: int = 0,
     workspace: int = 0,
     workspace_bytes: int = 0,
     prof_events: int = 0,
@@ -89,6 +91,8 @@ def make_desc(
     d.max_seqlen = max_seqlen
     d.dtype = dtype
     d.path = path
+    d.split_tokens = split_tokens
+    d.reserved = 0
     d.workspace = workspace or None
     d.workspace_bytes = workspace_bytes
     d.prof_events = prof_events or None
@@ -101,6 +105,10 @@ def workspace_size(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
 
 def num_splits_for(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
     return int(_lib.load().pkv_decode_num_splits(ctypes.byref(desc), int(num_splits)))
+
+
+def split_tokens_for(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
+    return int(_lib.load().pkv_decode_split_tokens(ctypes.byref(desc), int(num_splits)))
 
 
 def path_for(desc: PkvDecodeDesc) -> int:
@@ -126,6 +134,7 @@ def decode(
     *,
     max_seqlen: int = 0,
     path: int = PKV_PATH_AUTO,
+    split_tokens: int = 0,
     workspace=None,
     stream=None,
     prof_events: int = 0,
@@ -162,7 +171,7 @@ def decode(
     desc = make_desc(
         batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
         block_table_stride=block_table.shape[1], dtype=_dtype_code(q.dtype), max_seqlen=max_seqlen, path=path,
-        prof_events=prof_events,
+        split_tokens=split_tokens, prof_events=prof_events,
     )
     need = workspace_size(desc, num_splits)
     if need > 0:

@@ -32,6 +32,7 @@ EXPORTS = {
     "pkv_decode": (ctypes.c_int, None),  # argtypes filled below (needs the struct)
     "pkv_decode_workspace_size": (ctypes.c_size_t, None),
     "pkv_decode_num_splits": (ctypes.c_int, None),
+    "pkv_decode_split_tokens": (ctypes.c_int, None),
     "pkv_decode_path": (ctypes.c_int, None),
     "pkv_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "run_kernel": (None, [ctypes.c_void_p] * 4 + [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 9),
@@ -53,6 +54,8 @@ class PkvDecodeDesc(ctypes.Structure):
         ("max_seqlen", ctypes.c_int64),
         ("dtype", ctypes.c_int32),
         ("path", ctypes.c_int32),
+        ("split_tokens", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("prof_events", ctypes.c_void_p),
@@ -91,6 +94,8 @@ def load() -> ctypes.CDLL:
     lib.pkv_decode_workspace_size.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_num_splits.restype = ctypes.c_int
     lib.pkv_decode_num_splits.argtypes = [desc_p, ctypes.c_int]
+    lib.pkv_decode_split_tokens.restype = ctypes.c_int
+    lib.pkv_decode_split_tokens.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_path.restype = ctypes.c_int
     lib.pkv_decode_path.argtypes = [desc_p]
     for name in ("pkv_strerror", "run_kernel", "pkv_last_status"):

@@ -32,6 +32,9 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax rescale touches them with VALU ops,
+    # and AGPR accumulators cost a copy each way around every such update.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
@@ -54,24 +57,29 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def build_library(verbose: bool = False, jobs: int = 4) -> Path:
-    """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds)."""
+def build_library(verbose: bool = False, jobs: int = 4, out: Path | None = None,
+                  defines: tuple[str, ...] = ()) -> Path:
+    """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds).
+
+    `out` / `defines` build a variant elsewhere (tuning experiments)."""
     hipcc = _hipcc()
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    lib_path = Path(out) if out else LIB_PATH
+    build_dir = BUILD_DIR if out is None else lib_path.parent / "_build"
+    build_dir.mkdir(parents=True, exist_ok=True)
+    lib_path.parent.mkdir(parents=True, exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = BUILD_DIR / (src.rsplit(".", 1)[0] + ".o")
+        obj = build_dir / (src.rsplit(".", 1)[0] + ".o")
         lang = ["-x", "hip"]
-        cmds.append([hipcc, *HIPCC_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIPCC_FLAGS, *[f"-D{d}" for d in defines], *lang, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = lib_path.with_suffix(".so.tmp")
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 def build_oracle(verbose: bool = False) -> Path:

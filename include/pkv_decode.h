@@ -59,6 +59,9 @@ typedef struct pkv_decode_desc {
                                    0 = block_table_stride * page_size.  Used only to choose splits. */
     int32_t dtype;              /* PKV_DTYPE_F16 or PKV_DTYPE_BF16 (q, caches and out share it) */
     int32_t path;               /* PKV_PATH_* */
+    int32_t split_tokens;       /* num_splits == 0 only: tokens per split window (multiple of 16);
+                                   0 = chosen by the library */
+    int32_t reserved;           /* must be 0 */
     void* workspace;            /* device memory for split partials; may be NULL when splits == 1 */
     size_t workspace_bytes;
     void* prof_events;          /* optional: hipEvent_t[3] recorded before the partition kernel,
@@ -73,8 +76,13 @@ typedef struct pkv_decode_desc {
  * north-star argument order and an explicit stream.
  *
  * num_splits follows flash-attn (scripts/evaluate_flashattn_submission.py:246):
- *   0 = heuristic, 1 = single pass writing `out` directly, n > 1 = forced
- *   (clamped to [1, min(PKV_MAX_SPLITS, pages of max_seqlen)]).
+ *   0 = heuristic: every row is cut into fixed windows of split_tokens tokens
+ *       (chosen from the shape and the 256 CUs), so ragged rows cost work in
+ *       proportion to their length;
+ *   1 = single pass writing `out` directly;
+ *   n > 1 = forced: each row's valid pages are divided into n near-equal
+ *       ranges as the reference does (clamped to [1, min(PKV_MAX_SPLITS,
+ *       pages of max_seqlen)]).
  * Rows with cache_seqlens[b] <= 0 produce zeros; a row with one token
  * reproduces that token's V row bit-for-bit (best_flashattn_kvcache_decode.cu:256-283).
  * Asynchronous on `stream` (NULL = the null stream); no host synchronisation.
@@ -94,6 +102,11 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits);
  * Replaces choose_splits (best_flashattn_kvcache_decode.cu:1039-1076, 1299-1312).
  * Returns 0 if desc is invalid. */
 int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits);
+
+/* Tokens per split window pkv_decode will use for `num_splits` (0 when the
+ * splits are page-balanced or there is a single split).  No counterpart in
+ * the reference, which only has page-balanced splits. */
+int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits);
 
 /* Kernel family pkv_decode will use for this desc (resolves PKV_PATH_AUTO). */
 int pkv_decode_path(const pkv_decode_desc* desc);

@@ -55,6 +55,8 @@ def test_status_strings():
     ("num_pages", 0, pagedkv.PKV_EINVAL),
     ("block_table_stride", 0, pagedkv.PKV_EINVAL),
     ("path", 9, pagedkv.PKV_EINVAL),
+    ("split_tokens", 17, pagedkv.PKV_EINVAL),        # not a multiple of 16
+    ("split_tokens", -16, pagedkv.PKV_EINVAL),
 ])
 def test_invalid_descriptors_are_rejected_before_any_launch(field, value, status):
     lib = _lib.load()
@@ -133,3 +135,32 @@ def test_run_kernel_rejects_unsupported_modes_without_launching():
     assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
     lib.run_kernel(p, p, p, p, p, p, 4, 128, 1, 32, 8, 96, 16, 64, 0)    # head_dim 96
     assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
+
+
+def test_split_token_windows():
+    d = base_desc()
+    # heuristic: fixed windows, a power of two of at least 256 tokens
+    tok = pagedkv.split_tokens_for(d, 0)
+    assert tok >= 256 and tok & (tok - 1) == 0
+    assert pagedkv.num_splits_for(d, 0) == -(-4096 // tok)
+    # an explicit window is honoured
+    d = base_desc(split_tokens=512)
+    assert pagedkv.split_tokens_for(d, 0) == 512
+    assert pagedkv.num_splits_for(d, 0) == 8
+    # forced split counts are page-balanced (no window)
+    assert pagedkv.split_tokens_for(d, 4) == 0
+    # a window covering the longest row means one pass, no workspace
+    d = base_desc(split_tokens=4096)
+    assert pagedkv.num_splits_for(d, 0) == 1
+    assert pagedkv.split_tokens_for(d, 0) == 0
+    assert pagedkv.workspace_size(d, 0) == 0
+    # too many windows: the window grows so at most PKV_MAX_SPLITS remain
+    d = base_desc(max_seqlen=1 << 20, block_table_stride=1 << 14, split_tokens=16)
+    assert pagedkv.num_splits_for(d, 0) <= pagedkv.PKV_MAX_SPLITS
+    assert pagedkv.split_tokens_for(d, 0) % 16 == 0
+
+
+def test_reserved_field_must_be_zero():
+    d = base_desc()
+    d.reserved = 1
+    assert pagedkv.num_splits_for(d, 0) == 0

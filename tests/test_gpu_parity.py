@@ -39,14 +39,14 @@ def from_dev(t) -> np.ndarray:
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def run_hip(q, k, v, bt, sl, scale, dtype, num_splits=0, path=0, max_seqlen=0):
+def run_hip(q, k, v, bt, sl, scale, dtype, num_splits=0, path=0, max_seqlen=0, split_tokens=0):
     import pagedkv
 
     torch = torch_mod()
     out = pagedkv.decode(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype),
                          torch.from_numpy(np.ascontiguousarray(bt)).cuda(),
                          torch.from_numpy(np.ascontiguousarray(sl)).cuda(), scale, num_splits,
-                         max_seqlen=max_seqlen, path=path)
+                         max_seqlen=max_seqlen, path=path, split_tokens=split_tokens)
     torch.cuda.synchronize()
     return from_dev(out)
 
@@ -160,6 +160,18 @@ def test_split_count_invariance(rng, path):
     outs = [po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, 0, s, path), 0) for s in (1, 2, 7, 64, 188)]
     for o in outs[1:]:
         assert np.max(np.abs(o - outs[0])) <= 2 * 2.0 ** -11 * max(1.0, float(np.abs(outs[0]).max()))
+
+
+@pytest.mark.parametrize("path", PATHS)
+@pytest.mark.parametrize("split_tokens", [16, 48, 256, 1024])
+def test_token_window_splits_match_oracle(rng, path, split_tokens):
+    """num_splits = 0 with explicit windows: ragged rows, rows shorter than a window, empty rows."""
+    announce("windows", path, split_tokens)
+    q, k, v, bt, sl = make_case(rng, B=5, H=16, Hk=2, D=128, P=16, seqlens=[700, 1, 0, 33, 1500], dtype=1)
+    got = po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, 1, 0, path, split_tokens=split_tokens), 1)
+    want = po.decode_f64(q, k, v, bt, sl, 0.088, 1)
+    assert np.max(np.abs(got - want)) < TOL[1]
+    assert (got[2] == 0).all()
 
 
 @pytest.mark.parametrize("path", PATHS)
