@@ -130,10 +130,16 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     torch.cuda.synchronize()
     events.hip.hipEventRecord(t_start, sh)
     for i in range(K):
-        call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p))
+        call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p) if args.kernel_events else None)
     events.hip.hipEventRecord(t_end, sh)
     torch.cuda.synchronize()
     total_ms = events.elapsed_ms(t_start, t_end)
+    if not args.kernel_events:
+        # Kernel breakdown from a second, identical loop with the per-call events.
+        torch.cuda.synchronize()
+        for i in range(K):
+            call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p))
+        torch.cuda.synchronize()
     part_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) for i in range(K)]
     comb_ms = [events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) for i in range(K)]
     call_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 2]) for i in range(K)]
@@ -222,6 +228,9 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also measure every other config (extra lines to --json-out)")
     ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    ap.add_argument("--kernel-events", type=int, default=0,
+                    help="1: record the per-kernel HIP events inside the timed loop; 0: time the loop without "
+                         "them and take the kernel breakdown from a second identical loop")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of benchmarking, run a plain device copy of MIB MiB (read + write) five times; "

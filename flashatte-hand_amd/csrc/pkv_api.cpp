@@ -21,12 +21,16 @@ namespace {
 
 // gfx950 (MI355X) compute units; the split heuristic sizes grids against it.
 constexpr int kComputeUnits = 256;
-// Resident waves per CU the heuristic assumes for the partition kernel.
-constexpr int kWavesPerCU = 12;
-// Split windows are at least this long: shorter ones spend more on the item
-// prologue, the partial write and the combine than they gain in parallelism.
+
+// Split-window heuristic (tokens).  Measured on MI355X over the five
+// workload shapes: windows of 512 tokens beat shorter ones (each work item pays
+// a prologue of dependent loads and writes a partial), while the split count
+// per row is kept <= 64 because the combine's cost grows with it.
+constexpr int kBaseSplitTokens = 512;
 constexpr int kMinSplitTokens = 256;
-constexpr int kMaxSplitTokens = 8192;
+constexpr int kMaxSplitsPerRow = 64;
+// Below this many work items (4 per CU) the GPU is under-filled: shorten the window.
+constexpr int kMinItems = 4 * kComputeUnits;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
@@ -123,20 +127,20 @@ int64_t effective_max_seqlen(const pkv_decode_desc* d, const Resolved& r) {
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Window length for the heuristic: about two work items per resident wave
-// slot of the 256 CUs, assuming rows average half of max_seqlen, clamped to
-// [kMinSplitTokens, kMaxSplitTokens] and rounded to a power of two.  Unlike the
-// reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
-// it counts KV heads, head groups and the CU count, and equal windows keep
-// ragged rows from leaving a long tail of oversized items.
+// Window length for the heuristic: kBaseSplitTokens, lengthened (powers of
+// two) until the longest row has at most kMaxSplitsPerRow windows, then halved
+// (down to kMinSplitTokens) while fewer than kMinItems work items would exist.
+// Unlike the reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
+// it counts KV heads and head groups, and equal windows keep ragged rows from
+// leaving a long tail of oversized items.
 int64_t choose_split_tokens(const Resolved& r, int64_t max_seqlen) {
     const int64_t units = r.B * r.Hk * r.head_groups;
-    const int64_t slots = int64_t{kComputeUnits} * kWavesPerCU;
-    const int64_t est_tokens = units * std::max<int64_t>(1, max_seqlen / 2);
-    const int64_t want = est_tokens / (2 * slots);
-    int64_t tok = kMinSplitTokens;
-    while (tok < want && tok < kMaxSplitTokens) {
+    int64_t tok = kBaseSplitTokens;
+    while ((max_seqlen + tok - 1) / tok > kMaxSplitsPerRow) {
         tok *= 2;
+    }
+    while (tok > kMinSplitTokens && units * ((max_seqlen + tok - 1) / tok) < kMinItems) {
+        tok /= 2;
     }
     return tok;
 }

@@ -5,11 +5,14 @@
 // slots of empty splits are never read (whatever the workspace holds).  With
 // w_s = exp2(lse_s - max_s lse_s), out = (sum_s w_s o_s) * (1 / sum_s w_s),
 // cast RNE; a row without tokens gets zeros.  Partial rows are read in
-// batches of 8 splits so their loads are in flight together.
+// one batch so their loads are in flight together.
 // Reference: submission-oj/best_flashattn_kvcache_decode.cu:956-1037 and
 // v11_best_hybrid/flashattn_kvcache_decode_v11_best_hybrid.cu:604-613.
 #include "pkv_device.h"
 #include "pkv_launch.h"
+
+// Largest split count (PKV_MAX_SPLITS in include/pkv_decode.h).
+#define PKV_MAX_SPLITS_DEV 256
 
 namespace pkv {
 
@@ -18,10 +21,31 @@ __device__ __forceinline__ bool split_nonempty(const CombineParams& p, int seqle
     return r.begin < r.end;
 }
 
+template <int E>
+__device__ __forceinline__ void load_partial(const float* src, float (&x)[E]) {
+    if constexpr (E == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(src);
+        x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+    } else if constexpr (E == 2) {
+        const float2 t = *reinterpret_cast<const float2*>(src);
+        x[0] = t.x; x[1] = t.y;
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            x[e] = src[e];
+        }
+    }
+}
+
+// Two dependent memory round trips per row: cache_seqlens, then the partial
+// rows of the first kBatch splits together with the per-split LSEs (lane s
+// holds split s + 64k).  Weights reach every lane with readlane; partials are
+// folded in with a select, so an unused slot cannot inject NaN.
 template <bool BF16, int D>
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
     constexpr int E = D / 64; // output elements per lane
-    constexpr int kBatch = 8;
+    constexpr int kBatch = 16;
+    constexpr int kLseRegs = (PKV_MAX_SPLITS_DEV + 63) / 64;
     static_assert(E >= 1 && E <= 8, "head_dim must be 64..512");
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -34,19 +58,37 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
                            ? (seqlen > 0 ? min(p.splits, (seqlen + p.split_tokens - 1) / p.split_tokens) : 0)
                            : p.splits;
     const float* __restrict__ lse = p.part_lse + static_cast<int64_t>(row) * p.splits;
+    const float* __restrict__ o = p.part_o + static_cast<int64_t>(row) * p.splits * D + lane * E;
 
-    float mx = kNegInf;
-    for (int s = lane; s < n_loop; s += 64) {
-        if (split_nonempty(p, seqlen, s)) {
-            mx = fmaxf(mx, lse[s]);
+    // First batch of partial rows, issued before the LSE loads are consumed.
+    float x[kBatch][E];
+    bool ok[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+        ok[u] = u < n_loop && split_nonempty(p, seqlen, u);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            x[u][e] = 0.f;
         }
+        if (ok[u]) {
+            load_partial<E>(o + u * D, x[u]);
+        }
+    }
+
+    float lw[kLseRegs];
+    float mx = kNegInf;
+#pragma unroll
+    for (int k = 0; k < kLseRegs; ++k) {
+        const int s = lane + 64 * k;
+        lw[k] = (s < n_loop && split_nonempty(p, seqlen, s)) ? lse[s] : kNegInf;
+        mx = fmaxf(mx, lw[k]);
     }
     mx = group_max<64>(mx);
     float den = 0.f;
-    for (int s = lane; s < n_loop; s += 64) {
-        if (split_nonempty(p, seqlen, s)) {
-            den += fast_exp2(lse[s] - mx);
-        }
+#pragma unroll
+    for (int k = 0; k < kLseRegs; ++k) {
+        lw[k] = lw[k] == kNegInf ? 0.f : fast_exp2(lw[k] - mx); // weight of split lane + 64k
+        den += lw[k];
     }
     den = group_sum<64>(den);
     const float inv = den > 0.f ? 1.f / den : 0.f;
@@ -56,41 +98,30 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
     for (int e = 0; e < E; ++e) {
         acc[e] = 0.f;
     }
-    const float* __restrict__ o = p.part_o + static_cast<int64_t>(row) * p.splits * D + lane * E;
-    for (int s0 = 0; s0 < n_loop; s0 += kBatch) {
-        float w[kBatch];
-        float x[kBatch][E];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int s = s0 + u;
-            const bool use = s < n_loop && split_nonempty(p, seqlen, s);
-            w[u] = use ? fast_exp2(lse[s] - mx) : 0.f;
+    for (int u = 0; u < kBatch; ++u) {
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw[0]), u));
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                x[u][e] = 0.f;
-            }
-            if (use) {
-                const float* src = o + static_cast<int64_t>(s) * D;
-                if constexpr (E == 4) {
-                    const float4 t = *reinterpret_cast<const float4*>(src);
-                    x[u][0] = t.x; x[u][1] = t.y; x[u][2] = t.z; x[u][3] = t.w;
-                } else if constexpr (E == 2) {
-                    const float2 t = *reinterpret_cast<const float2*>(src);
-                    x[u][0] = t.x; x[u][1] = t.y;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        x[u][e] = src[e];
-                    }
-                }
-            }
+        for (int e = 0; e < E; ++e) {
+            acc[e] = ok[u] ? fmaf(w, x[u][e], acc[e]) : acc[e];
         }
+    }
+    for (int s = kBatch; s < n_loop; ++s) { // long rows: one split at a time
+        if (!split_nonempty(p, seqlen, s)) {
+            continue;
+        }
+        float y[E];
+        load_partial<E>(o + static_cast<int64_t>(s) * D, y);
+        int wk = 0;
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
+        for (int k = 1; k < kLseRegs; ++k) {
+            wk = s >= 64 * k ? __float_as_int(lw[k]) : wk;
+        }
+        const float wsel = s < 64 ? lw[0] : __int_as_float(wk);
+        const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsel), s & 63));
 #pragma unroll
-            for (int e = 0; e < E; ++e) {
-                acc[e] = fmaf(w[u], x[u][e], acc[e]);
-            }
+        for (int e = 0; e < E; ++e) {
+            acc[e] = fmaf(w, y[e], acc[e]);
         }
     }
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;

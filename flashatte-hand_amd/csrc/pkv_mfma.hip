@@ -88,32 +88,35 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams&
     constexpr int R = 64 / L;
     constexpr int NI = D / 32;
     const int rl = lane / L;
-    const int lane_off = kvh * D + 8 * (lane % L);
     const int pmask = (1 << p.page_shift) - 1;
+    const uint32_t col = static_cast<uint32_t>(kvh * D + 8 * (lane % L)) * 2u; // bytes within a token row
+    const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * 2u;            // bytes per token
     if constexpr (WIDE) {
+        // Wave-uniform page base (SGPRs) + 32-bit lane offsets: saddr-form loads.
         const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
         const int phys = __builtin_amdgcn_readlane(win, idx);
-        const int64_t base = real ? static_cast<int64_t>(phys) * p.page_stride : 0;
-        const uint16_t* kb = p.k + base;
-        const uint16_t* vb = p.v + base;
+        const int64_t base =
+            real ? (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(t0 & pmask) * p.token_stride) * 2
+                 : 0;
+        const char* kb = reinterpret_cast<const char*>(p.k) + base;
+        const char* vb = reinterpret_cast<const char*>(p.v) + base;
+        const int lim = real ? end - 1 - t0 : 0; // clamp: never touch unowned slots
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const int t = min(t0 + R * i + rl, end - 1); // clamp: never touch unowned slots
-            const int off = real ? (t & pmask) * static_cast<int>(p.token_stride) + lane_off : 0;
-            r.k[i] = load_kv16(kb + off);
-            r.v[i] = load_kv16(vb + off);
+            const uint32_t off = real ? static_cast<uint32_t>(min(R * i + rl, lim)) * ts2 + col : 0u;
+            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(kb + off));
+            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(vb + off));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int t = min(t0 + R * i + rl, end - 1);
             const int phys = __shfl(win, real ? (t >> p.page_shift) - win_base : 0, 64);
-            const int64_t off = real ? static_cast<int64_t>(phys) * p.page_stride +
-                                           static_cast<int64_t>((t & pmask) * static_cast<int>(p.token_stride) +
-                                                                lane_off)
-                                     : 0;
-            r.k[i] = load_kv16(p.k + off);
-            r.v[i] = load_kv16(p.v + off);
+            const int64_t off =
+                real ? static_cast<int64_t>(phys) * p.page_stride * 2 + static_cast<int64_t>(t & pmask) * ts2 + col
+                     : 0;
+            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.k) + off));
+            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.v) + off));
         }
     }
 }
@@ -130,13 +133,10 @@ struct VTile {
     static constexpr int kElems = 16 * kRow;
 };
 
-// Part 1 of a tile: stage the K and V rows in the wave's LDS tiles, read K back
-// in MFMA A-operand layout (lane (n, j): token n, dims 8(4kk + j) .. +7) and
-// compute S^T = K Q^T.  After this the tile's registers are free for the next
-// prefetch.
-template <bool BF16, int D>
-__device__ __forceinline__ f32x4 tile_scores(const TileRegs<D>& r, const uint4 (&qop)[D / 32], uint16_t* lds, int lane,
-                                             int n, int j) {
+// Part 1a of a tile: stage the K and V rows in the wave's LDS tiles.  After
+// this the tile's registers are free for the next prefetch.
+template <int D>
+__device__ __forceinline__ void stage_tile(const TileRegs<D>& r, uint16_t* lds, int lane) {
     constexpr int L = D / 8;
     constexpr int R = 64 / L;
     constexpr int NI = D / 32;
@@ -148,8 +148,14 @@ __device__ __forceinline__ f32x4 tile_scores(const TileRegs<D>& r, const uint4 (
         *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
         *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
     }
+}
+
+// Part 1b: read K back in MFMA A-operand layout (lane (n, j): token n, dims
+// 8(4kk + j) .. +7) and compute S^T = K Q^T.
+template <bool BF16, int D>
+__device__ __forceinline__ f32x4 tile_scores(const uint4 (&qop)[D / 32], const uint16_t* lds, int n, int j) {
     uint4 ka[D / 32];
-    const uint16_t* kr = kt + n * VTile<D>::kRow + 8 * j;
+    const uint16_t* kr = lds + n * VTile<D>::kRow + 8 * j;
 #pragma unroll
     for (int kk = 0; kk < D / 32; ++kk) {
         ka[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
@@ -245,13 +251,18 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
     // would be structurized through the loop header and make the compiler's
     // wait counts assume the just-issued prefetch is the tile being consumed.
     const int ntiles = (end - t + 15) >> 4;
+    // Per tile: stage the landed tile in LDS, immediately issue the prefetch
+    // into the freed registers (pinned there by a scheduling barrier), then
+    // compute.  The prefetch is in flight for the whole QK / softmax / PV.
     TileRegs<D> ra;
     load_tile<D, WIDE>(ra, p, win, win_base, t, end, true, lane, kvh);
     if constexpr (DEPTH == 1) {
         for (int k = 0; k < ntiles; ++k) {
-            const f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            stage_tile<D>(ra, lds, lane);
             ensure_window(t + 16);
             load_tile<D, WIDE>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
+            __builtin_amdgcn_sched_barrier(0);
+            const f32x4 s = tile_scores<BF16, D>(qop, lds, n, j);
             tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
             t += 16;
         }
@@ -260,26 +271,36 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
         ensure_window(t + 16);
         load_tile<D, WIDE>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
         for (int k = 0; k + 2 <= ntiles; k += 2) {
-            f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            stage_tile<D>(ra, lds, lane);
             ensure_window(t + 32);
             load_tile<D, WIDE>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 s = tile_scores<BF16, D>(qop, lds, n, j);
             tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
             t += 16;
-            s = tile_scores<BF16, D>(rb, qop, lds, lane, n, j);
+            stage_tile<D>(rb, lds, lane);
             ensure_window(t + 32);
             load_tile<D, WIDE>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
+            __builtin_amdgcn_sched_barrier(0);
+            s = tile_scores<BF16, D>(qop, lds, n, j);
             tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
             t += 16;
         }
         if (ntiles & 1) {
-            const f32x4 s = tile_scores<BF16, D>(ra, qop, lds, lane, n, j);
+            stage_tile<D>(ra, lds, lane);
+            const f32x4 s = tile_scores<BF16, D>(qop, lds, n, j);
             tile_softmax_pv<BF16, D>(s, o, m, l, lds, t, end, n, j, p.scale_log2);
         }
     }
 }
 
+#ifndef PKV_MFMA_WAVES_PER_EU
+#define PKV_MFMA_WAVES_PER_EU 1
+#endif
+
 template <bool BF16, int D, bool WIDE, int DEPTH>
-__global__ __launch_bounds__(64 * kWavesPerGroup) void partition_mfma_kernel(PartitionParams p) {
+__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(PKV_MFMA_WAVES_PER_EU)))
+void partition_mfma_kernel(PartitionParams p) {
     constexpr int KS = D / 32;
     constexpr int DT = D / 16;
     constexpr int kWaves = kWavesPerGroup;
