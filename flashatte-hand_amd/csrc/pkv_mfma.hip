@@ -325,6 +325,31 @@ void partition_mfma_kernel(PartitionParams p) {
     const int heads_here = min(16, p.group - g_first);
     const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
 
+    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+
+    // q and, with token windows, the page window do not depend on
+    // cache_seqlens, so their loads are issued together with its load: the
+    // item prologue costs two dependent round trips instead of three.
+    // B operand of QK: head n, dims 8(4kk + j) .. +7; zero columns past the group.
+    uint4 qop[KS];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        if (n < heads_here) {
+            qop[kk] = *reinterpret_cast<const uint4*>(p.q + (bh_first + n) * D + 8 * (4 * kk + j));
+        } else {
+            qop[kk] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    const bool windowed = p.split_tokens > 0;
+    int win_base = 0;
+    int win = 0;
+    if (windowed) {
+        // Entries past the row's last page are loaded too (ids are clamped to
+        // the pool) but never used for a valid token.
+        win_base = (split * p.split_tokens) >> p.page_shift;
+        win = load_page_window(bt_row, win_base, p.bt_stride - 1, lane, p.num_pages);
+    }
+
     const int seqlen = min(p.seqlens[b], p.row_cap);
     const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
 
@@ -344,20 +369,10 @@ void partition_mfma_kernel(PartitionParams p) {
     }
 
     const int end = range.end;
-    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
     const int last_page = (end - 1) >> p.page_shift;
-    int win_base = range.begin >> p.page_shift;
-    int win = load_page_window(bt_row, win_base, last_page, lane, p.num_pages);
-
-    // B operand of QK: head n, dims 8(4kk + j) .. +7; zero columns past the group.
-    uint4 qop[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-        if (n < heads_here) {
-            qop[kk] = *reinterpret_cast<const uint4*>(p.q + (bh_first + n) * D + 8 * (4 * kk + j));
-        } else {
-            qop[kk] = make_uint4(0u, 0u, 0u, 0u);
-        }
+    if (!windowed) {
+        win_base = range.begin >> p.page_shift;
+        win = load_page_window(bt_row, win_base, last_page, lane, p.num_pages);
     }
 
     f32x4 o[DT];
@@ -411,7 +426,7 @@ void partition_mfma_kernel(PartitionParams p) {
 }
 
 #ifndef PKV_MFMA_DEPTH
-#define PKV_MFMA_DEPTH 2
+#define PKV_MFMA_DEPTH 1
 #endif
 
 template <bool BF16, int D>
