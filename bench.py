@@ -59,6 +59,9 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
+SCHEDULES = {1: "single", 2: "pages", 3: "windows", 4: "tiles"}
+
+
 def percentile(xs, p):
     xs = sorted(xs)
     if not xs:
@@ -100,6 +103,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
     split_tokens = pagedkv.split_tokens_for(desc, splits_req)
+    schedule = SCHEDULES.get(pagedkv.schedule_for(desc, splits_req), "?")
     path = pagedkv.path_for(desc)
     ws_bytes = pagedkv.workspace_size(desc, splits_req)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
@@ -166,6 +170,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         "combine_us": sum(comb_ms) / K * 1e3,
         "splits": splits,
         "split_tokens": split_tokens,
+        "schedule": schedule,
         "path": {1: "valu", 2: "mfma"}.get(path, str(path)),
         "roofline": {
             "bound": "hbm",
@@ -278,7 +283,8 @@ def main() -> int:
             "vs_baseline": None,
             "dtype": cfg.dtype,
             "data": "synthetic (seeded N(0,1) values, random paged layout; see pagedkv/configs.py)",
-            "config": {**cfg.describe(), "splits": res["splits"], "split_tokens": res["split_tokens"],
+            "config": {**cfg.describe(), "schedule": res["schedule"], "splits": res["splits"],
+                       "split_tokens": res["split_tokens"],
                        "path": res["path"], "kv_sets": args.sets},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
@@ -298,7 +304,8 @@ def main() -> int:
         print(f"[bench] {name}: {line['us_per_call']} us/call, {line['value']} GB/s KV "
               f"({100 * line['hbm_frac_kv']:.1f}% of peak), partition {line['partition_us']} us "
               f"({100 * line['roofline']['frac']:.1f}% roofline), combine {line['combine_us']} us, "
-              f"splits {res['splits']} (window {res['split_tokens']}), path {res['path']}", file=sys.stderr, flush=True)
+              f"schedule {res['schedule']}, splits/workers {res['splits']} (window {res['split_tokens']}), "
+              f"path {res['path']}", file=sys.stderr, flush=True)
         del res
         torch.cuda.empty_cache()
     if args.json_out:

@@ -31,6 +31,10 @@ constexpr int kMinSplitTokens = 256;
 constexpr int kMaxSplitsPerRow = 64;
 // Below this many work items (4 per CU) the GPU is under-filled: shorten the window.
 constexpr int kMinItems = 4 * kComputeUnits;
+// Tile-balanced schedule: one workgroup of pkv::kTileWaves waves per CU, and
+// no fewer than this many 16-token tiles per wave (each wave's share starts
+// with a few dependent loads that more tiles amortise).
+constexpr int64_t kMinTilesPerWorker = 8;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
@@ -114,10 +118,11 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     return PKV_OK;
 }
 
-// How the rows are cut into splits for one call.
+// How the work of one call is divided.
 struct SplitPlan {
-    int splits;       // split slots per (b, h) row (0 = invalid request)
-    int split_tokens; // > 0: fixed token windows; 0: page-balanced splits
+    int schedule;     // PKV_SCHED_* (0 = invalid request)
+    int splits;       // split slots per (b, h) row; the worker count for PKV_SCHED_TILES
+    int split_tokens; // PKV_SCHED_WINDOWS: tokens per window
 };
 
 int64_t effective_max_seqlen(const pkv_decode_desc* d, const Resolved& r) {
@@ -145,12 +150,31 @@ int64_t choose_split_tokens(const Resolved& r, int64_t max_seqlen) {
     return tok;
 }
 
+// Streams of the tile-balanced schedule per row: (kv head, head group) pairs.
+int64_t streams_per_row(const Resolved& r) { return r.Hk * r.head_groups; }
+
+// Heads per partial slot of the tile-balanced schedule.
+int64_t part_heads(const Resolved& r) { return std::min<int64_t>(r.group, r.heads_per_wave); }
+
+// Waves of the tile-balanced schedule: one workgroup per CU, fewer when the
+// upper bound of the call's tiles (every row at max_seqlen) would leave a wave
+// with under kMinTilesPerWorker tiles.
+int tile_workers(const Resolved& r, int64_t max_seqlen) {
+    const int64_t tiles = r.B * streams_per_row(r) * ((max_seqlen + 15) / 16);
+    const int64_t per_group = kMinTilesPerWorker * pkv::kTileWaves;
+    const int64_t groups = std::clamp<int64_t>((tiles + per_group - 1) / per_group, 1, kComputeUnits);
+    return static_cast<int>(groups * pkv::kTileWaves);
+}
+
 SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
     if (num_splits < 0) {
-        return {0, 0};
+        return {0, 0, 0};
     }
     const int64_t max_seqlen = effective_max_seqlen(d, r);
     if (num_splits == 0) {
+        if (d->split_tokens == 0 && r.path == PKV_PATH_MFMA) {
+            return {PKV_SCHED_TILES, tile_workers(r, max_seqlen), 0};
+        }
         int64_t tok = d->split_tokens > 0 ? d->split_tokens : choose_split_tokens(r, max_seqlen);
         int64_t s = (max_seqlen + tok - 1) / tok;
         if (s > PKV_MAX_SPLITS) {
@@ -158,24 +182,37 @@ SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_sp
             s = (max_seqlen + tok - 1) / tok;
         }
         if (s <= 1) {
-            return {1, 0};
+            return {PKV_SCHED_SINGLE, 1, 0};
         }
-        return {static_cast<int>(s), static_cast<int>(tok)};
+        return {PKV_SCHED_WINDOWS, static_cast<int>(s), static_cast<int>(tok)};
     }
     int64_t s = std::min<int64_t>(num_splits, r.max_pages);
     s = std::min<int64_t>(s, PKV_MAX_SPLITS);
-    return {static_cast<int>(std::max<int64_t>(1, s)), 0};
+    s = std::max<int64_t>(1, s);
+    return {s == 1 ? PKV_SCHED_SINGLE : PKV_SCHED_PAGES, static_cast<int>(s), 0};
 }
 
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-size_t workspace_bytes(const Resolved& r, int splits) {
-    if (splits <= 1) {
+// Partial rows the plan stores: (b, h, split) rows for split schedules;
+// (workers + streams) slots of part_heads rows for the tile-balanced schedule.
+size_t partial_rows(const Resolved& r, const SplitPlan& plan) {
+    if (plan.schedule == PKV_SCHED_TILES) {
+        return static_cast<size_t>(plan.splits + r.B * streams_per_row(r)) * static_cast<size_t>(part_heads(r));
+    }
+    if (plan.schedule == PKV_SCHED_PAGES || plan.schedule == PKV_SCHED_WINDOWS) {
+        return static_cast<size_t>(r.B * r.H) * static_cast<size_t>(plan.splits);
+    }
+    return 0;
+}
+
+size_t workspace_bytes(const Resolved& r, const SplitPlan& plan) {
+    const size_t rows = partial_rows(r, plan);
+    if (rows == 0) {
         return 0;
     }
-    const size_t rows = static_cast<size_t>(r.B * r.H) * static_cast<size_t>(splits);
     return align_up(rows * static_cast<size_t>(r.D) * sizeof(float)) + align_up(rows * sizeof(float));
 }
 
@@ -220,6 +257,14 @@ int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
     return resolve_splits(desc, r, num_splits).split_tokens;
 }
 
+int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits).schedule;
+}
+
 int pkv_decode_path(const pkv_decode_desc* desc) {
     Resolved r;
     if (resolve(desc, r) != PKV_OK) {
@@ -233,8 +278,7 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    const SplitPlan plan = resolve_splits(desc, r, num_splits);
-    return workspace_bytes(r, plan.splits);
+    return workspace_bytes(r, resolve_splits(desc, r, num_splits));
 }
 
 int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
@@ -256,13 +300,14 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         return PKV_EINVAL;
     }
     const SplitPlan plan = resolve_splits(desc, r, num_splits);
-    const int splits = plan.splits;
-    const size_t need = workspace_bytes(r, splits);
+    const bool tiles = plan.schedule == PKV_SCHED_TILES;
+    const int splits = tiles ? 0 : plan.splits;
+    const size_t need = workspace_bytes(r, plan);
     if (need > 0 && (desc->workspace == nullptr || desc->workspace_bytes < need || !aligned16(desc->workspace))) {
         return PKV_ENOWORKSPACE;
     }
-    const int64_t items = r.B * r.Hk * r.head_groups * splits;
-    if (items > INT32_MAX) {
+    const int64_t items = tiles ? 0 : r.B * r.Hk * r.head_groups * splits;
+    if (items > INT32_MAX || (tiles && static_cast<int64_t>(plan.splits) + r.B * streams_per_row(r) > INT32_MAX)) {
         return PKV_EUNSUPPORTED;
     }
 
@@ -273,7 +318,7 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     p.block_table = block_table;
     p.seqlens = cache_seqlens;
     p.out = static_cast<uint16_t*>(out);
-    const size_t rows = static_cast<size_t>(r.B * r.H) * static_cast<size_t>(splits);
+    const size_t rows = partial_rows(r, plan);
     p.part_o = need > 0 ? static_cast<float*>(desc->workspace) : nullptr;
     p.part_lse = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(desc->workspace) +
                                                      align_up(rows * static_cast<size_t>(r.D) * sizeof(float)))
@@ -302,6 +347,8 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
 #define PKV_ITEM_ORDER 1
 #endif
     p.split_fastest = PKV_ITEM_ORDER == 1 ? 0 : PKV_ITEM_ORDER == 2 ? 1 : ((r.Hk * r.head_groups) % 8 == 0 ? 0 : 1);
+    p.tile_workers = tiles ? plan.splits : 0;
+    p.part_heads = static_cast<int32_t>(part_heads(r));
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
@@ -320,7 +367,7 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     if (ev != nullptr && hipEventRecord(ev[1], s) != hipSuccess) {
         return PKV_ELAUNCH;
     }
-    if (splits > 1) {
+    if (tiles || splits > 1) {
         pkv::CombineParams c{};
         c.part_o = p.part_o;
         c.part_lse = p.part_lse;
@@ -332,6 +379,11 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         c.split_tokens = plan.split_tokens;
         c.page_shift = r.page_shift;
         c.row_cap = p.row_cap;
+        c.tile_workers = p.tile_workers;
+        c.part_heads = p.part_heads;
+        c.batch = p.batch;
+        c.group = p.group;
+        c.head_groups = p.head_groups;
         if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s) != hipSuccess) {
             return PKV_ELAUNCH;
         }

@@ -131,11 +131,118 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
     }
 }
 
+// Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; its
+// workers w_a .. w_b are found from cache_seqlens with the partition's tile
+// arithmetic.  One worker means the partition already wrote the row; a row
+// without tokens gets zeros; otherwise the partials in slots w_a + r .. w_b + r
+// are merged: max and weight sum over their LSEs first, then the weighted rows
+// in batches of kBatch loads in flight.
+template <bool BF16, int D>
+__global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
+    constexpr int E = D / 64;
+    constexpr int kBatch = 16;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= p.rows) {
+        return;
+    }
+    const int b = row / p.num_heads;
+    const int h = row - b * p.num_heads;
+    const int kvh = h / p.group;
+    const int g = h - kvh * p.group;
+    const int hg = g / 16;
+    const int hn = g - 16 * hg;
+    const int spr = (p.num_heads / p.group) * p.head_groups;
+    const int u = kvh * p.head_groups + hg;
+    uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
+
+    const int nb = row_tiles(p.seqlens, b, p.row_cap);
+    if (nb == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            dst[e] = 0;
+        }
+        return;
+    }
+    int64_t before = 0;
+    int64_t all = 0;
+    for (int32_t bb = lane; bb < p.batch; bb += 64) {
+        const int32_t t = row_tiles(p.seqlens, bb, p.row_cap);
+        all += t;
+        before += bb < b ? t : 0;
+    }
+    before = uniform(wave_sum_i64(before));
+    const int64_t total = uniform(static_cast<int64_t>(spr) * wave_sum_i64(all));
+    const int64_t first = static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * nb;
+    const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
+    const int32_t wa = tile_worker_of(first, total, workers);
+    const int32_t wb = tile_worker_of(first + nb - 1, total, workers);
+    if (wa == wb) {
+        return;
+    }
+    const int parts = wb - wa + 1;
+    const int64_t slot0 = static_cast<int64_t>(wa) + static_cast<int64_t>(b) * spr + u;
+    const float* __restrict__ lse = p.part_lse + slot0 * p.part_heads + hn;
+    const float* __restrict__ po = p.part_o + (slot0 * p.part_heads + hn) * D + lane * E;
+    const int64_t lse_stride = p.part_heads;
+    const int64_t o_stride = static_cast<int64_t>(p.part_heads) * D;
+
+    float mx = kNegInf;
+    for (int k = lane; k < parts; k += 64) {
+        mx = fmaxf(mx, lse[k * lse_stride]);
+    }
+    mx = group_max<64>(mx);
+    float den = 0.f;
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        acc[e] = 0.f;
+    }
+    for (int k0 = 0; k0 < parts; k0 += 64) {
+        // Weight of part k0 + lane; every part has at least one token, so its LSE is finite.
+        const float wl = k0 + lane < parts ? fast_exp2(lse[(k0 + lane) * lse_stride] - mx) : 0.f;
+        den += wl;
+        const int chunk = min(64, parts - k0);
+        for (int c0 = 0; c0 < chunk; c0 += kBatch) {
+            float x[kBatch][E];
+#pragma unroll
+            for (int v = 0; v < kBatch; ++v) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    x[v][e] = 0.f;
+                }
+                if (c0 + v < chunk) {
+                    load_partial<E>(po + (k0 + c0 + v) * o_stride, x[v]);
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < kBatch; ++v) {
+                const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), (c0 + v) & 63));
+                const float wsel = c0 + v < chunk ? wv : 0.f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    acc[e] = fmaf(wsel, x[v][e], acc[e]);
+                }
+            }
+        }
+    }
+    den = group_sum<64>(den);
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+}
+
 template <bool BF16, int D>
 static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream) {
     constexpr int kWaves = 4;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
-    hipLaunchKernelGGL((combine_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    if (p.tile_workers > 0) {
+        hipLaunchKernelGGL((combine_tiles_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((combine_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    }
     return hipGetLastError();
 }
 

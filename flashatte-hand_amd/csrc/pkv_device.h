@@ -38,6 +38,8 @@ struct PartitionParams {
     int32_t num_items;    // splits * B * Hk * head_groups
     int32_t num_groups;   // workgroups in the grid (a multiple of 8)
     int32_t split_fastest; // item order: 1 = split index fastest, 0 = (kv head, head group) fastest
+    int32_t tile_workers; // > 0: tile-balanced schedule with this many waves (see TileSchedule)
+    int32_t part_heads;   // heads per partial slot in the tile-balanced schedule
     float scale_log2;     // softmax_scale * log2(e)
 };
 
@@ -52,6 +54,13 @@ struct CombineParams {
     int32_t split_tokens; // as in PartitionParams
     int32_t page_shift;
     int32_t row_cap;
+    // Tile-balanced schedule (tile_workers > 0); the fields above that name
+    // splits are then unused.
+    int32_t tile_workers;
+    int32_t part_heads;
+    int32_t batch;
+    int32_t group;        // H / Hk
+    int32_t head_groups;  // streams per (b, kv head)
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();
@@ -276,6 +285,12 @@ struct Item {
 #endif
 constexpr int kWavesPerGroup = PKV_WAVES_PER_GROUP;
 
+// Waves per workgroup of the tile-balanced partition kernel.
+#ifndef PKV_TILE_WAVES
+#define PKV_TILE_WAVES 8
+#endif
+constexpr int kTileWaves = PKV_TILE_WAVES;
+
 __device__ __forceinline__ int32_t wave_item(const PartitionParams& p) {
     const int32_t wave = static_cast<int32_t>(threadIdx.x >> 6);
     if (PKV_STRIDED_ITEMS) {
@@ -302,6 +317,100 @@ __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams&
     it.kvh = u / p.head_groups;
     it.hg = u - it.kvh * p.head_groups;
     return it;
+}
+
+// ---------------------------------------------------------------- tile-balanced schedule
+//
+// A stream is the work of one (b, kv head, head group): the n_b = ceil(seqlen_b / 16)
+// tiles of 16 tokens of row b.  Streams are numbered r = b * spr + u with
+// u = kv head * head_groups + head group (spr streams per row) and laid end to
+// end in that order, so the call is one sequence of T = spr * sum_b n_b tiles
+// and row b owns tiles [spr * C_b, spr * C_(b+1)) with C_b = sum_(b' < b) n_b'.
+// Worker w of W takes tiles [lo(w), lo(w + 1)), lo(w) = floor(w T / W): every
+// worker streams the same number of tiles (+-1) whatever the row lengths.
+// W is the launch's worker count clamped to T, so every worker owns a tile.
+// A worker's share crosses stream boundaries; each piece of a stream it
+// processes is a segment.  A segment that is a whole stream is written to the
+// output directly; otherwise it leaves a partial in slot w + r, which is
+// unique: the workers of stream r are the consecutive w_a(r) .. w_b(r), and
+// w_a(r + 1) >= w_b(r).  The combine finds a stream's workers with
+// w(x) = floor(((x + 1) W - 1) / T), the worker owning tile x.
+
+__device__ __forceinline__ int32_t row_tiles(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap) {
+    return (min(max(seqlens[b], 0), row_cap) + 15) >> 4;
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        x += __shfl_xor(x, d, 64);
+    }
+    return x;
+}
+
+// Sum of n_b over rows b < limit (every lane gets it).
+__device__ __forceinline__ int64_t tiles_before(const int32_t* __restrict__ seqlens, int32_t limit, int32_t row_cap,
+                                                int32_t lane) {
+    int64_t s = 0;
+    for (int32_t b = lane; b < limit; b += 64) {
+        s += row_tiles(seqlens, b, row_cap);
+    }
+    return wave_sum_i64(s);
+}
+
+// Worker owning tile x.
+__device__ __forceinline__ int32_t tile_worker_of(int64_t x, int64_t total, int32_t workers) {
+    return static_cast<int32_t>(((x + 1) * workers - 1) / total);
+}
+
+// Row holding row-tile index y (0 <= y < sum_b n_b): b, its clamped seqlen,
+// n_b and C_b.  Rows without tokens own no tiles and are never returned.
+struct RowTiles {
+    int32_t b;
+    int32_t seqlen;
+    int32_t n;
+    int64_t before;
+};
+
+__device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqlens, int32_t batch, int32_t row_cap,
+                                               int64_t y, int32_t lane) {
+    int64_t carry = 0;
+    for (int32_t base = 0; base < batch; base += 64) {
+        const int32_t b = base + lane;
+        const int32_t sl = b < batch ? min(max(seqlens[b], 0), row_cap) : 0;
+        const int32_t n = (sl + 15) >> 4;
+        int64_t incl = n;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int64_t t = __shfl_up(incl, d, 64);
+            incl += lane >= d ? t : 0;
+        }
+        incl += carry;
+        const uint64_t hit = __ballot(b < batch && incl > y);
+        if (hit != 0) {
+            const int32_t l = __builtin_ctzll(hit);
+            RowTiles r;
+            r.b = base + l;
+            r.seqlen = __shfl(sl, l, 64);
+            r.n = __shfl(n, l, 64);
+            r.before = __shfl(incl, l, 64) - r.n;
+            return r;
+        }
+        carry = __shfl(incl, 63, 64);
+    }
+    RowTiles r; // not reached for y < sum_b n_b
+    r.b = batch - 1;
+    r.seqlen = 0;
+    r.n = 0;
+    r.before = carry;
+    return r;
+}
+
+__device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ int64_t uniform(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Page-id window: lane l holds the physical id of logical page base + l of the

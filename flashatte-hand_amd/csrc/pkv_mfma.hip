@@ -294,10 +294,88 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
     }
 }
 
+// QK B operand: head n of the slice starting at bh_first, dims 8(4kk + j) .. +7;
+// zero columns past the slice's heads_here heads.
+template <int D>
+__device__ __forceinline__ void load_q_operand(const PartitionParams& p, int64_t bh_first, int heads_here, int n,
+                                               int j, uint4 (&qop)[D / 32]) {
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+        if (n < heads_here) {
+            qop[kk] = *reinterpret_cast<const uint4*>(p.q + (bh_first + n) * D + 8 * (4 * kk + j));
+        } else {
+            qop[kk] = make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+}
+
+// Attention of one head slice over tokens [begin, end) (begin < end), the page
+// window already loaded at win_base = begin / P.  Leaves the unnormalised O^T
+// tiles, the reference max m and the softmax denominator l (summed over the
+// tile rows, so every lane of head n holds it).
+template <bool BF16, int D, bool WIDE, int DEPTH>
+__device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
+                                             int win_base, const uint4 (&qop)[D / 32], uint16_t* lds, int begin,
+                                             int end, int lane, int kvh, f32x4 (&o)[D / 16], float& m, float& l) {
+    const int n = lane & 15;
+    const int j = lane >> 4;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    m = kNegInf;
+    l = 0.f;
+    const int last_page = (end - 1) >> p.page_shift;
+    if (last_page - win_base < 64) {
+        // Common case: the whole range fits in one page window.
+        tile_loop<BF16, D, WIDE, DEPTH, false>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, begin, end,
+                                               lane, n, j, kvh);
+    } else {
+        tile_loop<BF16, D, WIDE, DEPTH, true>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, begin, end,
+                                              lane, n, j, kvh);
+    }
+    // l holds this lane's 4-token partial sums; total over the 4 lanes of head n.
+    l = sum_halves32(sum_rows16(l));
+}
+
+// Output row of head bh: O / l rounded to 16 bits (RNE); lane (n, j) writes
+// dims 16 dt + 4j .. +3.
+template <bool BF16, int D>
+__device__ __forceinline__ void write_final(const PartitionParams& p, int64_t bh, const f32x4 (&o)[D / 16], float l,
+                                            int j) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* dst = p.out + bh * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        uint2 w;
+        w.x = pack2<BF16>(o[dt][0] * inv, o[dt][1] * inv);
+        w.y = pack2<BF16>(o[dt][2] * inv, o[dt][3] * inv);
+        *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
+    }
+}
+
+// Partial pi: O / l in fp32 and the log2-domain LSE m + log2(l).
+template <int D>
+__device__ __forceinline__ void write_partial(const PartitionParams& p, int64_t pi, const f32x4 (&o)[D / 16],
+                                              float m, float l, int j) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float* dst = p.part_o + pi * D + 4 * j;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+        *reinterpret_cast<float4*>(dst + 16 * dt) =
+            make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+    }
+    if (j == 0) {
+        p.part_lse[pi] = l > 0.f ? m + fast_log2(l) : kNegInf;
+    }
+}
+
 #ifndef PKV_MFMA_WAVES_PER_EU
 #define PKV_MFMA_WAVES_PER_EU 1
 #endif
 
+// Split schedules (one split, page-balanced splits, token windows): one wave
+// per work item (b, kv head, head group, split).
 template <bool BF16, int D, bool WIDE, int DEPTH>
 __global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(PKV_MFMA_WAVES_PER_EU)))
 void partition_mfma_kernel(PartitionParams p) {
@@ -330,16 +408,8 @@ void partition_mfma_kernel(PartitionParams p) {
     // q and, with token windows, the page window do not depend on
     // cache_seqlens, so their loads are issued together with its load: the
     // item prologue costs two dependent round trips instead of three.
-    // B operand of QK: head n, dims 8(4kk + j) .. +7; zero columns past the group.
     uint4 qop[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-        if (n < heads_here) {
-            qop[kk] = *reinterpret_cast<const uint4*>(p.q + (bh_first + n) * D + 8 * (4 * kk + j));
-        } else {
-            qop[kk] = make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
+    load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
     const bool windowed = p.split_tokens > 0;
     int win_base = 0;
     int win = 0;
@@ -367,60 +437,111 @@ void partition_mfma_kernel(PartitionParams p) {
         }
         return;
     }
-
-    const int end = range.end;
-    const int last_page = (end - 1) >> p.page_shift;
     if (!windowed) {
         win_base = range.begin >> p.page_shift;
-        win = load_page_window(bt_row, win_base, last_page, lane, p.num_pages);
+        win = load_page_window(bt_row, win_base, (range.end - 1) >> p.page_shift, lane, p.num_pages);
     }
 
     f32x4 o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-        o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    float m = kNegInf;
-    float l = 0.f;
-
-    uint16_t* lds = lds_tiles[wave];
-
-    if (last_page - win_base < 64) {
-        // Common case: the whole range fits in one page window.
-        tile_loop<BF16, D, WIDE, DEPTH, false>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, range.begin,
-                                               end, lane, n, j, kvh);
-    } else {
-        tile_loop<BF16, D, WIDE, DEPTH, true>(p, bt_row, last_page, win, win_base, qop, o, m, l, lds, range.begin,
-                                              end, lane, n, j, kvh);
-    }
-
-    // l holds this lane's 4-token partial sums; total over the 4 lanes of head n.
-    l = sum_halves32(sum_rows16(l));
-
+    float m;
+    float l;
+    attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds_tiles[wave], range.begin, range.end, lane,
+                                       kvh, o, m, l);
     if (n >= heads_here) {
         return;
     }
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int64_t bh = bh_first + n;
     if (p.splits == 1) {
-        uint16_t* dst = p.out + bh * D + 4 * j;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            uint2 w;
-            w.x = pack2<BF16>(o[dt][0] * inv, o[dt][1] * inv);
-            w.y = pack2<BF16>(o[dt][2] * inv, o[dt][3] * inv);
-            *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
-        }
+        write_final<BF16, D>(p, bh_first + n, o, l, j);
     } else {
-        const int64_t pi = bh * p.splits + split;
-        float* dst = p.part_o + pi * D + 4 * j;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            *reinterpret_cast<float4*>(dst + 16 * dt) =
-                make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+        write_partial<D>(p, (bh_first + n) * p.splits + split, o, m, l, j);
+    }
+}
+
+// Tile-balanced schedule: wave w of p.tile_workers streams tiles
+// [floor(w T / W), floor((w + 1) T / W)) of the call's tile sequence (streams
+// and slots as defined with row_tiles in pkv_device.h), segment by segment.  A segment that is a
+// whole stream is written to the output; any other leaves a partial in slot
+// w + r.  The workgroup's LDS request is padded on the host so that one
+// workgroup occupies a CU: the dispatcher then spreads the grid over all CUs
+// instead of doubling some up while others idle.
+template <bool BF16, int D, bool WIDE, int DEPTH, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
+    constexpr int KS = D / 32;
+    constexpr int DT = D / 16;
+    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[WAVES][2 * VTile<D>::kElems];
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int n = lane & 15;
+    const int j = lane >> 4;
+    const int32_t w = static_cast<int32_t>(blockIdx.x) * WAVES + wave;
+    if (w >= p.tile_workers) {
+        return;
+    }
+    const int32_t spr = p.num_heads_k * p.head_groups;
+    const int64_t total = uniform(static_cast<int64_t>(spr) * tiles_before(p.seqlens, p.batch, p.row_cap, lane));
+    // Never more workers than tiles: then every worker owns at least one tile
+    // and a stream's workers are consecutive.
+    const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
+    if (w >= workers) {
+        return;
+    }
+    int64_t x = static_cast<int64_t>(w) * total / workers;
+    const int64_t x_end = static_cast<int64_t>(w + 1) * total / workers;
+    if (x >= x_end) {
+        return;
+    }
+    const RowTiles rt = locate_row(p.seqlens, p.batch, p.row_cap, x / spr, lane);
+    int b = uniform(rt.b);
+    int seqlen = uniform(rt.seqlen);
+    int nb = uniform(rt.n);
+    const int64_t rel = x - static_cast<int64_t>(spr) * uniform(rt.before);
+    int u = uniform(static_cast<int32_t>(rel / nb));
+    int off = uniform(static_cast<int32_t>(rel - static_cast<int64_t>(u) * nb));
+    uint16_t* lds = lds_tiles[wave];
+
+    while (true) {
+        const int seg = static_cast<int>(min(static_cast<int64_t>(nb - off), x_end - x));
+        const int kvh = u / p.head_groups;
+        const int hg = u - kvh * p.head_groups;
+        const int g_first = hg * 16;
+        const int heads_here = min(16, p.group - g_first);
+        const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
+        const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+        const int begin = off * 16;
+        const int end = min((off + seg) * 16, seqlen);
+
+        uint4 qop[KS];
+        load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
+        const int win_base = begin >> p.page_shift;
+        const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
+
+        f32x4 o[DT];
+        float m;
+        float l;
+        attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds, begin, end, lane, kvh, o, m, l);
+        if (n < heads_here) {
+            if (off == 0 && seg == nb) {
+                write_final<BF16, D>(p, bh_first + n, o, l, j);
+            } else {
+                const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
+                write_partial<D>(p, slot * p.part_heads + n, o, m, l, j);
+            }
         }
-        if (j == 0) {
-            p.part_lse[pi] = l > 0.f ? m + fast_log2(l) : kNegInf;
+        x += seg;
+        if (x >= x_end) {
+            break;
+        }
+        // The stream is exhausted (x < x_end): move to the next stream, past
+        // rows without tokens.
+        off = 0;
+        if (++u == spr) {
+            u = 0;
+            do {
+                ++b;
+                seqlen = uniform(min(max(p.seqlens[b], 0), p.row_cap));
+            } while (seqlen == 0 && b + 1 < p.batch);
+            nb = (seqlen + 15) >> 4;
         }
     }
 }
@@ -429,11 +550,37 @@ void partition_mfma_kernel(PartitionParams p) {
 #define PKV_MFMA_DEPTH 1
 #endif
 
+#ifndef PKV_TILE_ONE_GROUP_PER_CU
+#define PKV_TILE_ONE_GROUP_PER_CU 1
+#endif
+
+template <bool BF16, int D, bool WIDE>
+static void launch_tiles_t(const PartitionParams& p, hipStream_t stream) {
+    constexpr int kWaves = kTileWaves;
+    const int blocks = (p.tile_workers + kWaves - 1) / kWaves;
+    // More than half of the CU's 160 KB of LDS per workgroup: at most one
+    // workgroup per CU.
+    constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
+    constexpr size_t kHalf = 80 * 1024;
+    const size_t dyn = PKV_TILE_ONE_GROUP_PER_CU && kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
+    hipLaunchKernelGGL((partition_tiles_kernel<BF16, D, WIDE, PKV_MFMA_DEPTH, kWaves>), dim3(blocks),
+                       dim3(64 * kWaves), dyn, stream, p);
+}
+
 template <bool BF16, int D>
 static hipError_t launch_mfma_t(const PartitionParams& p, hipStream_t stream) {
     constexpr int kWaves = kWavesPerGroup;
+    const bool wide = p.page_shift >= 4;
+    if (p.tile_workers > 0) {
+        if (wide) {
+            launch_tiles_t<BF16, D, true>(p, stream);
+        } else {
+            launch_tiles_t<BF16, D, false>(p, stream);
+        }
+        return hipGetLastError();
+    }
     const int blocks = p.num_groups;
-    if (p.page_shift >= 4) {
+    if (wide) {
         hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves), 0,
                            stream, p);
     } else {

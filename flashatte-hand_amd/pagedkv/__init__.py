@@ -31,6 +31,10 @@ from ._lib import (  # noqa: F401  (re-exported constants)
     PKV_PATH_AUTO,
     PKV_PATH_MFMA,
     PKV_PATH_VALU,
+    PKV_SCHED_PAGES,
+    PKV_SCHED_SINGLE,
+    PKV_SCHED_TILES,
+    PKV_SCHED_WINDOWS,
     PkvDecodeDesc,
     PkvError,
 )
@@ -43,6 +47,7 @@ __all__ = [
     "workspace_size",
     "num_splits_for",
     "split_tokens_for",
+    "schedule_for",
     "path_for",
     "PkvError",
 ]
@@ -109,6 +114,10 @@ def num_splits_for(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
 
 def split_tokens_for(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
     return int(_lib.load().pkv_decode_split_tokens(ctypes.byref(desc), int(num_splits)))
+
+
+def schedule_for(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
+    return int(_lib.load().pkv_decode_schedule(ctypes.byref(desc), int(num_splits)))
 
 
 def path_for(desc: PkvDecodeDesc) -> int:

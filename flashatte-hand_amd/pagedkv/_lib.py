@@ -25,6 +25,11 @@ PKV_PATH_AUTO = 0
 PKV_PATH_VALU = 1
 PKV_PATH_MFMA = 2
 
+PKV_SCHED_SINGLE = 1
+PKV_SCHED_PAGES = 2
+PKV_SCHED_WINDOWS = 3
+PKV_SCHED_TILES = 4
+
 PKV_MAX_SPLITS = 256
 
 # Every function the header declares, with its ctypes signature.
@@ -33,6 +38,7 @@ EXPORTS = {
     "pkv_decode_workspace_size": (ctypes.c_size_t, None),
     "pkv_decode_num_splits": (ctypes.c_int, None),
     "pkv_decode_split_tokens": (ctypes.c_int, None),
+    "pkv_decode_schedule": (ctypes.c_int, None),
     "pkv_decode_path": (ctypes.c_int, None),
     "pkv_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "run_kernel": (None, [ctypes.c_void_p] * 4 + [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 9),
@@ -96,6 +102,8 @@ def load() -> ctypes.CDLL:
     lib.pkv_decode_num_splits.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_split_tokens.restype = ctypes.c_int
     lib.pkv_decode_split_tokens.argtypes = [desc_p, ctypes.c_int]
+    lib.pkv_decode_schedule.restype = ctypes.c_int
+    lib.pkv_decode_schedule.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_path.restype = ctypes.c_int
     lib.pkv_decode_path.argtypes = [desc_p]
     for name in ("pkv_strerror", "run_kernel", "pkv_last_status"):

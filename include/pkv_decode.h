@@ -43,6 +43,12 @@ extern "C" {
 #define PKV_PATH_VALU 1        /* VALU dot2 products + DPP row reductions */
 #define PKV_PATH_MFMA 2        /* gfx950 16x16x32 / 16x16x16 MFMA for QK^T and PV */
 
+/* Work schedules (pkv_decode_schedule). */
+#define PKV_SCHED_SINGLE 1     /* one pass per (b, kv head, head group); out written directly */
+#define PKV_SCHED_PAGES 2      /* each row's pages cut into num_splits near-equal ranges (the reference's) */
+#define PKV_SCHED_WINDOWS 3    /* each row cut into fixed windows of split_tokens tokens */
+#define PKV_SCHED_TILES 4      /* the call's 16-token tiles dealt evenly to a fixed set of waves */
+
 /* Largest split count a single call may use (the reference caps at 64,
  * best_flashattn_kvcache_decode.cu:15). */
 #define PKV_MAX_SPLITS 256
@@ -76,9 +82,13 @@ typedef struct pkv_decode_desc {
  * north-star argument order and an explicit stream.
  *
  * num_splits follows flash-attn (scripts/evaluate_flashattn_submission.py:246):
- *   0 = heuristic: every row is cut into fixed windows of split_tokens tokens
- *       (chosen from the shape and the 256 CUs), so ragged rows cost work in
- *       proportion to their length;
+ *   0 = heuristic: on the MFMA path with desc->split_tokens == 0, the
+ *       tile-balanced schedule — all rows' 16-token tiles (times KV heads and
+ *       head groups) are laid end to end and dealt in equal shares to one
+ *       workgroup of waves per CU, which read cache_seqlens on the device, so
+ *       every wave streams the same bytes however ragged the rows are, and a
+ *       combine merges the rows that more than one wave touched.  Otherwise
+ *       fixed windows of split_tokens tokens (chosen from the shape when 0);
  *   1 = single pass writing `out` directly;
  *   n > 1 = forced: each row's valid pages are divided into n near-equal
  *       ranges as the reference does (clamped to [1, min(PKV_MAX_SPLITS,
@@ -98,10 +108,16 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache,
  * hidden grow-only workspace (best_flashattn_kvcache_decode.cu:17-20, 1078-1133). */
 size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits);
 
-/* Split count pkv_decode will use for `num_splits` (0 = heuristic).
+/* Split count pkv_decode will use for `num_splits` (0 = heuristic); for
+ * PKV_SCHED_TILES, the number of partition waves sharing the tiles.
  * Replaces choose_splits (best_flashattn_kvcache_decode.cu:1039-1076, 1299-1312).
  * Returns 0 if desc is invalid. */
 int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits);
+
+/* Schedule (PKV_SCHED_*) pkv_decode will use for `num_splits`; 0 if desc is
+ * invalid.  The reference has only single-pass and page-balanced splits
+ * (best_flashattn_kvcache_decode.cu:664-671, 1299-1312). */
+int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits);
 
 /* Tokens per split window pkv_decode will use for `num_splits` (0 when the
  * splits are page-balanced or there is a single split).  No counterpart in

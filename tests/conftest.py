@@ -35,11 +35,12 @@ def rand_bits(rng: np.random.Generator, shape, dtype: int, sigma: float = 1.0) -
     return pkv_oracle.f32_to_bits(x, dtype)
 
 
-def make_case(rng: np.random.Generator, *, B, H, Hk, D, P, seqlens, dtype, pool_extra=3, sigma=1.0):
-    """Small paged case: distinct scattered pages per row, unused table entries = -1."""
+def make_case(rng: np.random.Generator, *, B, H, Hk, D, P, seqlens, dtype, pool_extra=3, sigma=1.0, stride=1):
+    """Small paged case: distinct scattered pages per row, unused table entries = -1.
+    The block table has at least `stride` columns."""
     seqlens = np.asarray(seqlens, dtype=np.int32)
     pages = (np.maximum(seqlens, 0) + P - 1) // P
-    stride = max(1, int(pages.max()))
+    stride = max(stride, int(pages.max()))
     pool = int(pages.sum()) + pool_extra
     perm = rng.permutation(pool).astype(np.int32)
     bt = np.full((B, stride), -1, dtype=np.int32)

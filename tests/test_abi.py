@@ -93,7 +93,7 @@ def test_missing_workspace_is_reported():
 
 
 def test_workspace_size_formula():
-    d = base_desc()
+    d = base_desc()   # forced splits: (b, h, split) rows
     for s in (1, 2, 8, 64):
         got = pagedkv.workspace_size(d, s)
         if s == 1:
@@ -111,14 +111,47 @@ def test_split_resolution():
     assert pagedkv.num_splits_for(d, 10_000) == 64          # clamped to the pages of max_seqlen
     d2 = base_desc(max_seqlen=100_000, block_table_stride=4096)
     assert pagedkv.num_splits_for(d2, 10_000) == pagedkv.PKV_MAX_SPLITS
-    auto = pagedkv.num_splits_for(d, 0)
+    assert pagedkv.schedule_for(d, 1) == pagedkv.PKV_SCHED_SINGLE
+    assert pagedkv.schedule_for(d, 7) == pagedkv.PKV_SCHED_PAGES
+    # window heuristic (VALU path, or an explicit window)
+    v = base_desc(path=pagedkv.PKV_PATH_VALU)
+    assert pagedkv.schedule_for(v, 0) == pagedkv.PKV_SCHED_WINDOWS
+    auto = pagedkv.num_splits_for(v, 0)
     assert 1 <= auto <= 64
     # short rows never split below the minimum split length
-    assert pagedkv.num_splits_for(base_desc(max_seqlen=200), 0) == 1
+    assert pagedkv.num_splits_for(base_desc(max_seqlen=200, path=pagedkv.PKV_PATH_VALU), 0) == 1
+    assert pagedkv.schedule_for(base_desc(max_seqlen=200, path=pagedkv.PKV_PATH_VALU), 0) == pagedkv.PKV_SCHED_SINGLE
     # tiny batch with a long context gets many splits, capped by PKV_MAX_SPLITS
     many = pagedkv.num_splits_for(base_desc(batch=1, num_heads=8, num_heads_k=1, max_seqlen=131072,
-                                            block_table_stride=2048), 0)
+                                            block_table_stride=2048, path=pagedkv.PKV_PATH_VALU), 0)
     assert 64 <= many <= pagedkv.PKV_MAX_SPLITS
+
+
+TILE_WAVES = 8      # waves per workgroup of the tile-balanced kernel
+COMPUTE_UNITS = 256
+
+
+def test_tile_schedule_plan():
+    d = base_desc()                                          # MFMA path (auto), no explicit window
+    assert pagedkv.path_for(d) == pagedkv.PKV_PATH_MFMA
+    assert pagedkv.schedule_for(d, 0) == pagedkv.PKV_SCHED_TILES
+    assert pagedkv.split_tokens_for(d, 0) == 0
+    # one workgroup per CU once there are >= 8 tiles per wave
+    assert pagedkv.num_splits_for(d, 0) == COMPUTE_UNITS * TILE_WAVES
+    # small calls: fewer workgroups, at least 8 tiles per wave (upper bound from max_seqlen)
+    small = base_desc(batch=1, num_heads=8, num_heads_k=2, max_seqlen=256, block_table_stride=4)
+    tiles = 1 * 2 * 1 * (256 // 16)                          # B * Hk * head groups * tiles per row
+    assert pagedkv.num_splits_for(small, 0) == -(-tiles // (8 * TILE_WAVES)) * TILE_WAVES
+    # workspace: (workers + streams) slots of min(16, group) heads, fp32 rows + LSEs
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for desc, group in ((d, 4), (base_desc(num_heads=64, num_heads_k=2), 32)):
+        workers = pagedkv.num_splits_for(desc, 0)
+        streams = 32 * desc.num_heads_k * -(-group // 16)
+        rows = (workers + streams) * min(16, group)
+        assert pagedkv.workspace_size(desc, 0) == align(rows * 128 * 4) + align(rows * 4)
+    # an explicit window or forced splits leave the tile schedule
+    assert pagedkv.schedule_for(base_desc(split_tokens=512), 0) == pagedkv.PKV_SCHED_WINDOWS
+    assert pagedkv.schedule_for(d, 4) == pagedkv.PKV_SCHED_PAGES
 
 
 def test_auto_path_is_a_kernel_family():
@@ -138,15 +171,16 @@ def test_run_kernel_rejects_unsupported_modes_without_launching():
 
 
 def test_split_token_windows():
-    d = base_desc()
+    d = base_desc(path=pagedkv.PKV_PATH_VALU)
     # heuristic: fixed windows, a power of two of at least 256 tokens
     tok = pagedkv.split_tokens_for(d, 0)
     assert tok >= 256 and tok & (tok - 1) == 0
     assert pagedkv.num_splits_for(d, 0) == -(-4096 // tok)
-    # an explicit window is honoured
-    d = base_desc(split_tokens=512)
-    assert pagedkv.split_tokens_for(d, 0) == 512
-    assert pagedkv.num_splits_for(d, 0) == 8
+    # an explicit window is honoured (on either path)
+    for path in (pagedkv.PKV_PATH_VALU, pagedkv.PKV_PATH_MFMA):
+        d = base_desc(split_tokens=512, path=path)
+        assert pagedkv.split_tokens_for(d, 0) == 512
+        assert pagedkv.num_splits_for(d, 0) == 8
     # forced split counts are page-balanced (no window)
     assert pagedkv.split_tokens_for(d, 4) == 0
     # a window covering the longest row means one pass, no workspace

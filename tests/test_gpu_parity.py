@@ -89,7 +89,7 @@ def test_small_cases_match_oracle(rng, path, splits, B, H, Hk, D, P, seqlens, dt
 def test_single_token_rows_copy_v_bit_exact(rng, path, dtype):
     announce("seqlen1", path, dtype)
     q, k, v, bt, sl = make_case(rng, B=4, H=16, Hk=4, D=128, P=16, seqlens=[1, 1, 0, 1], dtype=dtype)
-    for splits in (1, 4):
+    for splits in (1, 4, 0):
         out = run_hip(q, k, v, bt, sl, 0.088, dtype, splits, path, max_seqlen=64)
         for b in (0, 1, 3):
             for h in range(16):
@@ -107,7 +107,7 @@ def test_dominant_key_returns_its_value_row_bit_exact(rng, path, dtype):
     stars = [(0, 13), (1, 128)]
     for b, t in stars:
         k[bt[b, t // 16], t % 16, :, :] = po.f32_to_bits(np.full((2, 128), 4.0, np.float32), dtype)
-    for splits in (1, 5):
+    for splits in (1, 5, 0):
         out = run_hip(q, k, v, bt, sl, 1.0, dtype, splits, path)
         for b, t in stars:
             for h in range(8):
@@ -121,7 +121,7 @@ def test_page_permutation_is_bit_exact(rng, path):
     perm = rng.permutation(k.shape[0])
     inv = np.argsort(perm)
     bt2 = np.where(bt >= 0, inv[np.maximum(bt, 0)], -1).astype(np.int32)
-    for splits in (1, 4):
+    for splits in (1, 4, 0):
         a = run_hip(q, k, v, bt, sl, 0.088, 1, splits, path)
         b = run_hip(q, k[perm], v[perm], bt2, sl, 0.088, 1, splits, path)
         assert (a == b).all()
@@ -157,7 +157,7 @@ def test_nan_poison_outside_valid_tokens(rng, path, dtype):
 def test_split_count_invariance(rng, path):
     announce("split-invariance", path)
     q, k, v, bt, sl = make_case(rng, B=2, H=32, Hk=8, D=128, P=16, seqlens=[3000, 1777], dtype=0)
-    outs = [po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, 0, s, path), 0) for s in (1, 2, 7, 64, 188)]
+    outs = [po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, 0, s, path), 0) for s in (1, 2, 7, 64, 188, 0)]
     for o in outs[1:]:
         assert np.max(np.abs(o - outs[0])) <= 2 * 2.0 ** -11 * max(1.0, float(np.abs(outs[0]).max()))
 
@@ -172,6 +172,74 @@ def test_token_window_splits_match_oracle(rng, path, split_tokens):
     want = po.decode_f64(q, k, v, bt, sl, 0.088, 1)
     assert np.max(np.abs(got - want)) < TOL[1]
     assert (got[2] == 0).all()
+
+
+# ------------------------------------------------------------------ tile-balanced schedule (MFMA, num_splits = 0)
+
+def _schedule(B, H, Hk, D, P, max_seqlen, stride):
+    import pagedkv
+
+    d = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=1,
+                          block_table_stride=stride, dtype=1, max_seqlen=max_seqlen, path=2)
+    return pagedkv.schedule_for(d, 0), pagedkv.num_splits_for(d, 0)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_tiles_ragged_rows_past_one_wave_of_rows(rng, dtype):
+    """70 rows (more than one 64-row chunk of the device-side scan): empty rows,
+    one-token rows, rows shorter than a tile and rows spread over many workers."""
+    lens = rng.integers(0, 1200, size=70)
+    lens[[0, 5, 63, 64, 69]] = [0, 1, 0, 1, 2500]
+    lens[10:14] = 0
+    q, k, v, bt, sl = make_case(rng, B=70, H=16, Hk=2, D=128, P=16, seqlens=lens.tolist(), dtype=dtype)
+    sched, workers = _schedule(70, 16, 2, 128, 16, int(sl.max()), bt.shape[1])
+    announce("tiles-ragged", dtype, "schedule", sched, "workers", workers)
+    assert sched == 4
+    got = po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, dtype, 0, 2, max_seqlen=int(sl.max())), dtype)
+    want = po.decode_f64(q, k, v, bt, sl, 0.088, dtype)
+    err = float(np.max(np.abs(got - want)))
+    print(f"max_abs_err={err:.3e}")
+    assert err < TOL[dtype]
+    assert (got[sl == 0] == 0).all()
+
+
+def test_tiles_one_long_row_many_partials(rng):
+    """One row of 20000 tokens: more than 64 partials per output row in the combine."""
+    q, k, v, bt, sl = make_case(rng, B=1, H=8, Hk=1, D=128, P=64, seqlens=[20000], dtype=0)
+    sched, workers = _schedule(1, 8, 1, 128, 64, 20000, bt.shape[1])
+    announce("tiles-long-row", "workers", workers)
+    assert sched == 4 and workers > 64
+    got = po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.088, 0, 0, 2, max_seqlen=20000), 0)
+    want = po.decode_f64(q, k, v, bt, sl, 0.088, 0)
+    assert np.max(np.abs(got - want)) < TOL[0]
+
+
+def test_tiles_more_workers_than_tiles(rng):
+    """max_seqlen unknown (0): the plan assumes full rows and launches far more
+    workers than the call has tiles; the device clamps to one tile per worker."""
+    q, k, v, bt, sl = make_case(rng, B=3, H=8, Hk=2, D=64, P=16, seqlens=[5, 40, 0], dtype=1, stride=512)
+    sched, workers = _schedule(3, 8, 2, 64, 16, 0, bt.shape[1])
+    announce("tiles-few-tiles", "workers", workers)
+    assert sched == 4 and workers > 2 * (1 + 3)
+    got = po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.125, 1, 0, 2), 1)
+    want = po.decode_f64(q, k, v, bt, sl, 0.125, 1)
+    assert np.max(np.abs(got - want)) < TOL[1]
+    assert (got[2] == 0).all()
+
+
+def test_tiles_all_rows_empty(rng):
+    q, k, v, bt, sl = make_case(rng, B=4, H=8, Hk=2, D=128, P=16, seqlens=[0, 0, 0, 0], dtype=1)
+    announce("tiles-empty")
+    out = run_hip(q, k, v, bt, sl, 0.088, 1, 0, 2, max_seqlen=64)
+    assert (out == 0).all()
+
+
+def test_tiles_deterministic(rng):
+    q, k, v, bt, sl = make_case(rng, B=6, H=32, Hk=8, D=128, P=64, seqlens=[3000, 1, 700, 2049, 0, 64], dtype=1)
+    announce("tiles-deterministic")
+    a = run_hip(q, k, v, bt, sl, 0.088, 1, 0, 2)
+    b = run_hip(q, k, v, bt, sl, 0.088, 1, 0, 2)
+    assert (a == b).all()
 
 
 @pytest.mark.parametrize("path", PATHS)
