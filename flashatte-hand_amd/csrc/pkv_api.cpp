@@ -19,8 +19,8 @@
 
 namespace {
 
-// gfx950 (MI355X) compute units; the split heuristic sizes grids against it.
-constexpr int kComputeUnits = 256;
+// gfx950 (MI355X) compute units; the split heuristics size grids against it.
+constexpr int kComputeUnits = pkv::kComputeUnits;
 
 // Split-window heuristic (tokens).  Measured on MI355X over the five
 // workload shapes: windows of 512 tokens beat shorter ones (each work item pays

@@ -285,9 +285,14 @@ struct Item {
 #endif
 constexpr int kWavesPerGroup = PKV_WAVES_PER_GROUP;
 
-// Waves per workgroup of the tile-balanced partition kernel.
+// Compute units of gfx950 (MI355X): grids are sized against it.
+constexpr int kComputeUnits = 256;
+
+// Waves per workgroup (= per CU) of the tile-balanced partition kernel.
+// Measured on MI355X over the five workload shapes: 4 (one per SIMD) streams
+// faster than 2, 3 or 8, and than 4 with two tiles of prefetch per wave.
 #ifndef PKV_TILE_WAVES
-#define PKV_TILE_WAVES 8
+#define PKV_TILE_WAVES 4
 #endif
 constexpr int kTileWaves = PKV_TILE_WAVES;
 
@@ -404,6 +409,60 @@ __device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqle
     r.n = 0;
     r.before = carry;
     return r;
+}
+
+// Inclusive prefix sum over the wave's lanes.
+__device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t t = __shfl_up(x, d, 64);
+        x += lane >= d ? t : 0;
+    }
+    return x;
+}
+
+// Start of one worker's share: the call's tile count T and the row holding
+// tile x = floor(w T / W).  Rows 0..63 are read once and kept in registers
+// (one load round trip for batches up to 64 rows); larger batches add a sum
+// over the remaining rows and a second, chunked pass to locate the row.
+struct WorkerStart {
+    int64_t total;
+    RowTiles row;
+};
+
+__device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __restrict__ seqlens, int32_t batch,
+                                                           int32_t row_cap, int32_t spr, int32_t w,
+                                                           int32_t workers, int32_t lane) {
+    const int32_t sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
+    const int32_t n0 = (sl0 + 15) >> 4;
+    const int64_t incl0 = wave_inclusive_scan(n0, lane);
+    int64_t rows_total = __shfl(incl0, 63, 64);
+    if (batch > 64) {
+        int64_t rest = 0;
+        for (int32_t b = lane + 64; b < batch; b += 64) {
+            rest += row_tiles(seqlens, b, row_cap);
+        }
+        rows_total += wave_sum_i64(rest);
+    }
+    WorkerStart ws;
+    ws.total = static_cast<int64_t>(spr) * rows_total;
+    const int64_t eff = min(static_cast<int64_t>(workers), ws.total);
+    if (w >= eff) {
+        ws.row.b = -1;
+        return ws;
+    }
+    const int64_t y = static_cast<int64_t>(w) * ws.total / eff / spr;
+    const uint64_t hit = __ballot(lane < batch && incl0 > y);
+    if (hit != 0) {
+        const int32_t l = __builtin_ctzll(hit);
+        ws.row.b = l;
+        ws.row.seqlen = __shfl(sl0, l, 64);
+        ws.row.n = __shfl(n0, l, 64);
+        ws.row.before = __shfl(incl0, l, 64) - ws.row.n;
+    } else {
+        ws.row = locate_row(seqlens, batch, row_cap, y, lane);
+    }
+    return ws;
 }
 
 __device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }

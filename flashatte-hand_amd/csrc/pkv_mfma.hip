@@ -479,7 +479,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         return;
     }
     const int32_t spr = p.num_heads_k * p.head_groups;
-    const int64_t total = uniform(static_cast<int64_t>(spr) * tiles_before(p.seqlens, p.batch, p.row_cap, lane));
+    const WorkerStart start = locate_worker_start(p.seqlens, p.batch, p.row_cap, spr, w, p.tile_workers, lane);
+    const int64_t total = uniform(start.total);
     // Never more workers than tiles: then every worker owns at least one tile
     // and a stream's workers are consecutive.
     const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
@@ -488,14 +489,10 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
     }
     int64_t x = static_cast<int64_t>(w) * total / workers;
     const int64_t x_end = static_cast<int64_t>(w + 1) * total / workers;
-    if (x >= x_end) {
-        return;
-    }
-    const RowTiles rt = locate_row(p.seqlens, p.batch, p.row_cap, x / spr, lane);
-    int b = uniform(rt.b);
-    int seqlen = uniform(rt.seqlen);
-    int nb = uniform(rt.n);
-    const int64_t rel = x - static_cast<int64_t>(spr) * uniform(rt.before);
+    int b = uniform(start.row.b);
+    int seqlen = uniform(start.row.seqlen);
+    int nb = uniform(start.row.n);
+    const int64_t rel = x - static_cast<int64_t>(spr) * uniform(start.row.before);
     int u = uniform(static_cast<int32_t>(rel / nb));
     int off = uniform(static_cast<int32_t>(rel - static_cast<int64_t>(u) * nb));
     uint16_t* lds = lds_tiles[wave];
@@ -546,9 +543,13 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
     }
 }
 
+// Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
+// whole chip busy and streams fastest with one; the split schedules take two
+// when their few waves (fewer than one per CU) are latency-bound.
 #ifndef PKV_MFMA_DEPTH
 #define PKV_MFMA_DEPTH 1
 #endif
+constexpr int kSplitDepthFewItems = 2;
 
 #ifndef PKV_TILE_ONE_GROUP_PER_CU
 #define PKV_TILE_ONE_GROUP_PER_CU 1
@@ -580,12 +581,23 @@ static hipError_t launch_mfma_t(const PartitionParams& p, hipStream_t stream) {
         return hipGetLastError();
     }
     const int blocks = p.num_groups;
+    const bool few = p.num_items < kComputeUnits;
     if (wide) {
-        hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves), 0,
-                           stream, p);
+        if (few) {
+            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, kSplitDepthFewItems>), dim3(blocks),
+                               dim3(64 * kWaves), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves),
+                               0, stream, p);
+        }
     } else {
-        hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves),
-                           0, stream, p);
+        if (few) {
+            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, kSplitDepthFewItems>), dim3(blocks),
+                               dim3(64 * kWaves), 0, stream, p);
+        } else {
+            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, PKV_MFMA_DEPTH>), dim3(blocks),
+                               dim3(64 * kWaves), 0, stream, p);
+        }
     }
     return hipGetLastError();
 }

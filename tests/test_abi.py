@@ -127,7 +127,7 @@ def test_split_resolution():
     assert 64 <= many <= pagedkv.PKV_MAX_SPLITS
 
 
-TILE_WAVES = 8      # waves per workgroup of the tile-balanced kernel
+TILE_WAVES = 4      # waves per workgroup of the tile-balanced kernel
 COMPUTE_UNITS = 256
 
 
