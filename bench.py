@@ -127,26 +127,25 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         call(i)
     torch.cuda.synchronize()
 
-    # Timed region: K calls, per-call events around the partition kernel and the combine.
+    # Timed region: K calls bracketed by two events, nothing else on the stream.
     K = args.steps
-    evs = events.create(3 * K)
+    evs = events.create(4 * K)
     t_start, t_end = events.create(2)
     torch.cuda.synchronize()
     events.hip.hipEventRecord(t_start, sh)
     for i in range(K):
-        call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p) if args.kernel_events else None)
+        call(i)
     events.hip.hipEventRecord(t_end, sh)
     torch.cuda.synchronize()
     total_ms = events.elapsed_ms(t_start, t_end)
-    if not args.kernel_events:
-        # Kernel breakdown from a second, identical loop with the per-call events.
-        torch.cuda.synchronize()
-        for i in range(K):
-            call(i, ctypes.addressof(evs) + 3 * i * ctypes.sizeof(ctypes.c_void_p))
-        torch.cuda.synchronize()
-    part_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 1]) for i in range(K)]
-    comb_ms = [events.elapsed_ms(evs[3 * i + 1], evs[3 * i + 2]) for i in range(K)]
-    call_ms = [events.elapsed_ms(evs[3 * i], evs[3 * i + 2]) for i in range(K)]
+    # Kernel breakdown from a second, identical loop: each kernel's dispatch
+    # packet records its own start / end events (no marker packets in between).
+    for i in range(K):
+        call(i, ctypes.addressof(evs) + 4 * i * ctypes.sizeof(ctypes.c_void_p))
+    torch.cuda.synchronize()
+    part_ms = [events.elapsed_ms(evs[4 * i], evs[4 * i + 1]) for i in range(K)]
+    comb_ms = [events.elapsed_ms(evs[4 * i + 2], evs[4 * i + 3]) for i in range(K)]
+    call_ms = [events.elapsed_ms(evs[4 * i], evs[4 * i + 3]) for i in range(K)]
     events.destroy(evs)
     events.destroy([t_start, t_end])
 
@@ -233,9 +232,6 @@ def main() -> int:
     ap.add_argument("--all", action="store_true", help="also measure every other config (extra lines to --json-out)")
     ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
-    ap.add_argument("--kernel-events", type=int, default=0,
-                    help="1: record the per-kernel HIP events inside the timed loop; 0: time the loop without "
-                         "them and take the kernel breakdown from a second identical loop")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of benchmarking, run a plain device copy of MIB MiB (read + write) five times; "
@@ -244,7 +240,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(decode shards with no communication; see DESIGN.md).", file=sys.stderr)
+              "(decode shards over (b, kv head) with no communication).", file=sys.stderr)
         return 2
 
     import torch

@@ -354,17 +354,18 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipEvent_t* ev = static_cast<hipEvent_t*>(desc->prof_events);
+    pkv::LaunchEvents part_ev;
+    pkv::LaunchEvents comb_ev;
+    if (ev != nullptr) {
+        part_ev = {ev[0], ev[1]};
+        comb_ev = {ev[2], ev[3]};
+    }
 
-    if (ev != nullptr && hipEventRecord(ev[0], s) != hipSuccess) {
-        return PKV_ELAUNCH;
-    }
-    hipError_t e = r.path == PKV_PATH_MFMA
-                       ? pkv::launch_partition_mfma(p, bf16, static_cast<int>(r.D), s)
-                       : pkv::launch_partition_valu(p, bf16, static_cast<int>(r.D), r.heads_per_wave, s);
+    const hipError_t e = r.path == PKV_PATH_MFMA
+                             ? pkv::launch_partition_mfma(p, bf16, static_cast<int>(r.D), s, part_ev)
+                             : pkv::launch_partition_valu(p, bf16, static_cast<int>(r.D), r.heads_per_wave, s,
+                                                          part_ev);
     if (e != hipSuccess) {
-        return PKV_ELAUNCH;
-    }
-    if (ev != nullptr && hipEventRecord(ev[1], s) != hipSuccess) {
         return PKV_ELAUNCH;
     }
     if (tiles || splits > 1) {
@@ -384,12 +385,14 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         c.batch = p.batch;
         c.group = p.group;
         c.head_groups = p.head_groups;
-        if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s) != hipSuccess) {
+        if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s, comb_ev) != hipSuccess) {
             return PKV_ELAUNCH;
         }
-    }
-    if (ev != nullptr && hipEventRecord(ev[2], s) != hipSuccess) {
-        return PKV_ELAUNCH;
+    } else if (ev != nullptr) {
+        // No combine: its events mark the end of the partition.
+        if (hipEventRecord(ev[2], s) != hipSuccess || hipEventRecord(ev[3], s) != hipSuccess) {
+            return PKV_ELAUNCH;
+        }
     }
     return PKV_OK;
 }

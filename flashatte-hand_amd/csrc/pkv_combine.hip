@@ -235,30 +235,31 @@ __global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
 }
 
 template <bool BF16, int D>
-static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream) {
+static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = 4;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
     if (p.tile_workers > 0) {
-        hipLaunchKernelGGL((combine_tiles_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+        launch_kernel(combine_tiles_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else {
-        hipLaunchKernelGGL((combine_kernel<BF16, D>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+        launch_kernel(combine_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream) {
+hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,
+                          const LaunchEvents& ev) {
     if (bf16) {
         switch (head_dim) {
-        case 64: return launch_combine_t<true, 64>(p, stream);
-        case 128: return launch_combine_t<true, 128>(p, stream);
-        case 256: return launch_combine_t<true, 256>(p, stream);
+        case 64: return launch_combine_t<true, 64>(p, stream, ev);
+        case 128: return launch_combine_t<true, 128>(p, stream, ev);
+        case 256: return launch_combine_t<true, 256>(p, stream, ev);
         default: return hipErrorInvalidValue;
         }
     }
     switch (head_dim) {
-    case 64: return launch_combine_t<false, 64>(p, stream);
-    case 128: return launch_combine_t<false, 128>(p, stream);
-    case 256: return launch_combine_t<false, 256>(p, stream);
+    case 64: return launch_combine_t<false, 64>(p, stream, ev);
+    case 128: return launch_combine_t<false, 128>(p, stream, ev);
+    case 256: return launch_combine_t<false, 256>(p, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }

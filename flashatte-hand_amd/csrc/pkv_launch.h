@@ -1,20 +1,43 @@
 // pkv_launch.h — host-side launchers of the device kernels (internal to the library).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include "pkv_device.h"
 
 namespace pkv {
 
+// Optional profiling events.  When set, the launch's own dispatch packet
+// records them as the kernel starts and completes (hipExtLaunchKernelGGL), so
+// their difference is the kernel's execution time without extra marker packets
+// on the stream.
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                          const LaunchEvents& ev, Args... args) {
+    if (ev.start != nullptr) {
+        hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, ev.start, ev.stop, 0u,
+                              args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream, args...);
+    }
+}
+
 // VALU partition kernel; heads_per_wave in {1, 2, 4, 8, 16}, head_dim in {64, 128, 256}.
 hipError_t launch_partition_valu(const PartitionParams& p, bool bf16, int head_dim, int heads_per_wave,
-                                 hipStream_t stream);
+                                 hipStream_t stream, const LaunchEvents& ev);
 
 // MFMA partition kernel; 16 heads per wave (zero-padded), head_dim in {64, 128, 256}.
-hipError_t launch_partition_mfma(const PartitionParams& p, bool bf16, int head_dim, hipStream_t stream);
+hipError_t launch_partition_mfma(const PartitionParams& p, bool bf16, int head_dim, hipStream_t stream,
+                                 const LaunchEvents& ev);
 
 // LSE combine of split partials into the 16-bit output.
-hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream);
+hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,
+                          const LaunchEvents& ev);
 
 } // namespace pkv

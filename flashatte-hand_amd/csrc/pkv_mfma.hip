@@ -556,7 +556,7 @@ constexpr int kSplitDepthFewItems = 2;
 #endif
 
 template <bool BF16, int D, bool WIDE>
-static void launch_tiles_t(const PartitionParams& p, hipStream_t stream) {
+static void launch_tiles_t(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = kTileWaves;
     const int blocks = (p.tile_workers + kWaves - 1) / kWaves;
     // More than half of the CU's 160 KB of LDS per workgroup: at most one
@@ -564,57 +564,56 @@ static void launch_tiles_t(const PartitionParams& p, hipStream_t stream) {
     constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
     constexpr size_t kHalf = 80 * 1024;
     const size_t dyn = PKV_TILE_ONE_GROUP_PER_CU && kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
-    hipLaunchKernelGGL((partition_tiles_kernel<BF16, D, WIDE, PKV_MFMA_DEPTH, kWaves>), dim3(blocks),
-                       dim3(64 * kWaves), dyn, stream, p);
+    launch_kernel(partition_tiles_kernel<BF16, D, WIDE, PKV_MFMA_DEPTH, kWaves>, dim3(blocks), dim3(64 * kWaves), dyn,
+                  stream, ev, p);
 }
 
 template <bool BF16, int D>
-static hipError_t launch_mfma_t(const PartitionParams& p, hipStream_t stream) {
+static hipError_t launch_mfma_t(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = kWavesPerGroup;
     const bool wide = p.page_shift >= 4;
     if (p.tile_workers > 0) {
         if (wide) {
-            launch_tiles_t<BF16, D, true>(p, stream);
+            launch_tiles_t<BF16, D, true>(p, stream, ev);
         } else {
-            launch_tiles_t<BF16, D, false>(p, stream);
+            launch_tiles_t<BF16, D, false>(p, stream, ev);
         }
         return hipGetLastError();
     }
     const int blocks = p.num_groups;
     const bool few = p.num_items < kComputeUnits;
+    const dim3 grid(blocks);
+    const dim3 block(64 * kWaves);
     if (wide) {
         if (few) {
-            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, kSplitDepthFewItems>), dim3(blocks),
-                               dim3(64 * kWaves), 0, stream, p);
+            launch_kernel(partition_mfma_kernel<BF16, D, true, kSplitDepthFewItems>, grid, block, 0, stream, ev, p);
         } else {
-            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>), dim3(blocks), dim3(64 * kWaves),
-                               0, stream, p);
+            launch_kernel(partition_mfma_kernel<BF16, D, true, PKV_MFMA_DEPTH>, grid, block, 0, stream, ev, p);
         }
     } else {
         if (few) {
-            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, kSplitDepthFewItems>), dim3(blocks),
-                               dim3(64 * kWaves), 0, stream, p);
+            launch_kernel(partition_mfma_kernel<BF16, D, false, kSplitDepthFewItems>, grid, block, 0, stream, ev, p);
         } else {
-            hipLaunchKernelGGL((partition_mfma_kernel<BF16, D, false, PKV_MFMA_DEPTH>), dim3(blocks),
-                               dim3(64 * kWaves), 0, stream, p);
+            launch_kernel(partition_mfma_kernel<BF16, D, false, PKV_MFMA_DEPTH>, grid, block, 0, stream, ev, p);
         }
     }
     return hipGetLastError();
 }
 
-hipError_t launch_partition_mfma(const PartitionParams& p, bool bf16, int head_dim, hipStream_t stream) {
+hipError_t launch_partition_mfma(const PartitionParams& p, bool bf16, int head_dim, hipStream_t stream,
+                                 const LaunchEvents& ev) {
     if (bf16) {
         switch (head_dim) {
-        case 64: return launch_mfma_t<true, 64>(p, stream);
-        case 128: return launch_mfma_t<true, 128>(p, stream);
-        case 256: return launch_mfma_t<true, 256>(p, stream);
+        case 64: return launch_mfma_t<true, 64>(p, stream, ev);
+        case 128: return launch_mfma_t<true, 128>(p, stream, ev);
+        case 256: return launch_mfma_t<true, 256>(p, stream, ev);
         default: return hipErrorInvalidValue;
         }
     }
     switch (head_dim) {
-    case 64: return launch_mfma_t<false, 64>(p, stream);
-    case 128: return launch_mfma_t<false, 128>(p, stream);
-    case 256: return launch_mfma_t<false, 256>(p, stream);
+    case 64: return launch_mfma_t<false, 64>(p, stream, ev);
+    case 128: return launch_mfma_t<false, 128>(p, stream, ev);
+    case 256: return launch_mfma_t<false, 256>(p, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }

@@ -202,40 +202,40 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void partition_valu_kernel(Par
 // ---------------------------------------------------------------- launchers
 
 template <bool BF16, int D, int GT>
-static hipError_t launch_valu_t(const PartitionParams& p, hipStream_t stream) {
+static hipError_t launch_valu_t(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int NT = GT <= 2 ? 8 : (GT <= 4 ? 8 : (GT <= 8 ? 4 : 2));
     constexpr int kWaves = kWavesPerGroup;
     const int blocks = p.num_groups;
-    hipLaunchKernelGGL((partition_valu_kernel<BF16, D, GT, NT>), dim3(blocks), dim3(64 * kWaves), 0, stream, p);
+    launch_kernel(partition_valu_kernel<BF16, D, GT, NT>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     return hipGetLastError();
 }
 
 template <bool BF16, int D>
-static hipError_t launch_valu_d(const PartitionParams& p, int gt, hipStream_t stream) {
+static hipError_t launch_valu_d(const PartitionParams& p, int gt, hipStream_t stream, const LaunchEvents& ev) {
     switch (gt) {
-    case 1: return launch_valu_t<BF16, D, 1>(p, stream);
-    case 2: return launch_valu_t<BF16, D, 2>(p, stream);
-    case 4: return launch_valu_t<BF16, D, 4>(p, stream);
-    case 8: return launch_valu_t<BF16, D, 8>(p, stream);
-    case 16: return launch_valu_t<BF16, D, 16>(p, stream);
+    case 1: return launch_valu_t<BF16, D, 1>(p, stream, ev);
+    case 2: return launch_valu_t<BF16, D, 2>(p, stream, ev);
+    case 4: return launch_valu_t<BF16, D, 4>(p, stream, ev);
+    case 8: return launch_valu_t<BF16, D, 8>(p, stream, ev);
+    case 16: return launch_valu_t<BF16, D, 16>(p, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_partition_valu(const PartitionParams& p, bool bf16, int head_dim, int heads_per_wave,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const LaunchEvents& ev) {
     if (bf16) {
         switch (head_dim) {
-        case 64: return launch_valu_d<true, 64>(p, heads_per_wave, stream);
-        case 128: return launch_valu_d<true, 128>(p, heads_per_wave, stream);
-        case 256: return launch_valu_d<true, 256>(p, heads_per_wave, stream);
+        case 64: return launch_valu_d<true, 64>(p, heads_per_wave, stream, ev);
+        case 128: return launch_valu_d<true, 128>(p, heads_per_wave, stream, ev);
+        case 256: return launch_valu_d<true, 256>(p, heads_per_wave, stream, ev);
         default: return hipErrorInvalidValue;
         }
     }
     switch (head_dim) {
-    case 64: return launch_valu_d<false, 64>(p, heads_per_wave, stream);
-    case 128: return launch_valu_d<false, 128>(p, heads_per_wave, stream);
-    case 256: return launch_valu_d<false, 256>(p, heads_per_wave, stream);
+    case 64: return launch_valu_d<false, 64>(p, heads_per_wave, stream, ev);
+    case 128: return launch_valu_d<false, 128>(p, heads_per_wave, stream, ev);
+    case 256: return launch_valu_d<false, 256>(p, heads_per_wave, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }

@@ -70,8 +70,10 @@ typedef struct pkv_decode_desc {
     int32_t reserved;           /* must be 0 */
     void* workspace;            /* device memory for split partials; may be NULL when splits == 1 */
     size_t workspace_bytes;
-    void* prof_events;          /* optional: hipEvent_t[3] recorded before the partition kernel,
-                                   after it and after the combine kernel (profiling only; NULL in use) */
+    void* prof_events;          /* optional: hipEvent_t[4] = partition start, partition end, combine
+                                   start, combine end, recorded by the kernels' own dispatch packets
+                                   (profiling only; NULL in use).  Without a combine, [2] and [3]
+                                   are recorded right after the partition. */
 } pkv_decode_desc;
 
 /*
