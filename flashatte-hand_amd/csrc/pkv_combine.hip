@@ -132,8 +132,8 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
 }
 
 // Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; its
-// workers w_a .. w_b are found from cache_seqlens with the partition's tile
-// arithmetic.  One worker means the partition already wrote the row; a row
+// workers w_a .. w_b are found from cache_seqlens with the partition's unit
+// arithmetic (the workers owning the stream's first and last tiles).  One worker means the partition already wrote the row; a row
 // without tokens gets zeros; otherwise the partials in slots w_a + r .. w_b + r
 // are merged: max and weight sum over their LSEs first, then the weighted rows
 // in batches of kBatch loads in flight.
@@ -167,13 +167,15 @@ __global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
     int64_t before = 0;
     int64_t all = 0;
     for (int32_t bb = lane; bb < p.batch; bb += 64) {
-        const int32_t t = row_tiles(p.seqlens, bb, p.row_cap);
+        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap));
         all += t;
         before += bb < b ? t : 0;
     }
     before = uniform(wave_sum_i64(before));
     const int64_t total = uniform(static_cast<int64_t>(spr) * wave_sum_i64(all));
-    const int64_t first = static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * nb;
+    // Unit of the stream's first tile.
+    const int64_t first =
+        static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
     const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
     const int32_t wa = tile_worker_of(first, total, workers);
     const int32_t wb = tile_worker_of(first + nb - 1, total, workers);

@@ -329,21 +329,36 @@ __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams&
 // A stream is the work of one (b, kv head, head group): the n_b = ceil(seqlen_b / 16)
 // tiles of 16 tokens of row b.  Streams are numbered r = b * spr + u with
 // u = kv head * head_groups + head group (spr streams per row) and laid end to
-// end in that order, so the call is one sequence of T = spr * sum_b n_b tiles
-// and row b owns tiles [spr * C_b, spr * C_(b+1)) with C_b = sum_(b' < b) n_b'.
-// Worker w of W takes tiles [lo(w), lo(w + 1)), lo(w) = floor(w T / W): every
-// worker streams the same number of tiles (+-1) whatever the row lengths.
-// W is the launch's worker count clamped to T, so every worker owns a tile.
-// A worker's share crosses stream boundaries; each piece of a stream it
-// processes is a segment.  A segment that is a whole stream is written to the
-// output directly; otherwise it leaves a partial in slot w + r, which is
-// unique: the workers of stream r are the consecutive w_a(r) .. w_b(r), and
-// w_a(r + 1) >= w_b(r).  The combine finds a stream's workers with
-// w(x) = floor(((x + 1) W - 1) / T), the worker owning tile x.
+// end in that order as units_b = stream_units(n_b) balancing units each
+// (kHeaderTiles header units, then the tiles), so the call is one sequence of
+// T = spr * sum_b units_b units and row b owns units [spr * C_b, spr * C_(b+1))
+// with C_b = sum_(b' < b) units_b'.  Worker w of W takes units [lo(w), lo(w + 1)),
+// lo(w) = floor(w T / W): every worker gets the same share (+-1) whatever the
+// row lengths.  W is the launch's worker count clamped to T, so every worker
+// owns a unit.  A worker's share crosses stream boundaries; the tiles of one
+// stream it owns are a segment.  A segment that is a whole stream is written
+// to the output directly; otherwise it leaves a partial in slot w + r, which
+// is unique: the workers owning stream r's tiles are the consecutive
+// w_a(r) .. w_b(r), and w_a(r + 1) >= w_b(r).  The combine finds them with
+// w(x) = floor(((x + 1) W - 1) / T), the worker owning unit x; tile t of
+// stream r is unit spr * C_b + u * units_b + kHeaderTiles + t.
 
 __device__ __forceinline__ int32_t row_tiles(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap) {
     return (min(max(seqlens[b], 0), row_cap) + 15) >> 4;
 }
+
+// Balancing units of a stream with n tiles: its tiles plus kHeaderTiles for
+// the dependent loads that start every segment (page window, first tile),
+// which cost about as much as a tile each.  A worker that starts a new stream
+// inside its share is charged for them, so workers with an extra segment do
+// not end up last.  The header units precede the stream's tiles and are never
+// processed.
+#ifndef PKV_HEADER_TILES
+#define PKV_HEADER_TILES 2
+#endif
+constexpr int32_t kHeaderTiles = PKV_HEADER_TILES;
+
+__device__ __forceinline__ int32_t stream_units(int32_t n) { return n > 0 ? n + kHeaderTiles : 0; }
 
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
 #pragma unroll
@@ -353,23 +368,14 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
     return x;
 }
 
-// Sum of n_b over rows b < limit (every lane gets it).
-__device__ __forceinline__ int64_t tiles_before(const int32_t* __restrict__ seqlens, int32_t limit, int32_t row_cap,
-                                                int32_t lane) {
-    int64_t s = 0;
-    for (int32_t b = lane; b < limit; b += 64) {
-        s += row_tiles(seqlens, b, row_cap);
-    }
-    return wave_sum_i64(s);
-}
 
 // Worker owning tile x.
 __device__ __forceinline__ int32_t tile_worker_of(int64_t x, int64_t total, int32_t workers) {
     return static_cast<int32_t>(((x + 1) * workers - 1) / total);
 }
 
-// Row holding row-tile index y (0 <= y < sum_b n_b): b, its clamped seqlen,
-// n_b and C_b.  Rows without tokens own no tiles and are never returned.
+// Row holding stream-unit index y (0 <= y < sum_b units_b): b, its clamped
+// seqlen, n_b and C_b.  Rows without tokens own no units and are never returned.
 struct RowTiles {
     int32_t b;
     int32_t seqlen;
@@ -384,7 +390,8 @@ __device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqle
         const int32_t b = base + lane;
         const int32_t sl = b < batch ? min(max(seqlens[b], 0), row_cap) : 0;
         const int32_t n = (sl + 15) >> 4;
-        int64_t incl = n;
+        const int32_t un = stream_units(n);
+        int64_t incl = un;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
             const int64_t t = __shfl_up(incl, d, 64);
@@ -398,7 +405,7 @@ __device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqle
             r.b = base + l;
             r.seqlen = __shfl(sl, l, 64);
             r.n = __shfl(n, l, 64);
-            r.before = __shfl(incl, l, 64) - r.n;
+            r.before = __shfl(incl, l, 64) - stream_units(r.n);
             return r;
         }
         carry = __shfl(incl, 63, 64);
@@ -421,8 +428,8 @@ __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) 
     return x;
 }
 
-// Start of one worker's share: the call's tile count T and the row holding
-// tile x = floor(w T / W).  Rows 0..63 are read once and kept in registers
+// Start of one worker's share: the call's unit count T and the row holding
+// unit x = floor(w T / W).  Rows 0..63 are read once and kept in registers
 // (one load round trip for batches up to 64 rows); larger batches add a sum
 // over the remaining rows and a second, chunked pass to locate the row.
 struct WorkerStart {
@@ -435,12 +442,12 @@ __device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __rest
                                                            int32_t workers, int32_t lane) {
     const int32_t sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
     const int32_t n0 = (sl0 + 15) >> 4;
-    const int64_t incl0 = wave_inclusive_scan(n0, lane);
+    const int64_t incl0 = wave_inclusive_scan(stream_units(n0), lane);
     int64_t rows_total = __shfl(incl0, 63, 64);
     if (batch > 64) {
         int64_t rest = 0;
         for (int32_t b = lane + 64; b < batch; b += 64) {
-            rest += row_tiles(seqlens, b, row_cap);
+            rest += stream_units(row_tiles(seqlens, b, row_cap));
         }
         rows_total += wave_sum_i64(rest);
     }
@@ -458,7 +465,7 @@ __device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __rest
         ws.row.b = l;
         ws.row.seqlen = __shfl(sl0, l, 64);
         ws.row.n = __shfl(n0, l, 64);
-        ws.row.before = __shfl(incl0, l, 64) - ws.row.n;
+        ws.row.before = __shfl(incl0, l, 64) - stream_units(ws.row.n);
     } else {
         ws.row = locate_row(seqlens, batch, row_cap, y, lane);
     }

@@ -481,57 +481,60 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
     const int32_t spr = p.num_heads_k * p.head_groups;
     const WorkerStart start = locate_worker_start(p.seqlens, p.batch, p.row_cap, spr, w, p.tile_workers, lane);
     const int64_t total = uniform(start.total);
-    // Never more workers than tiles: then every worker owns at least one tile
-    // and a stream's workers are consecutive.
+    // Never more workers than units: then every worker owns a unit and the
+    // workers owning a stream's tiles are consecutive.
     const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
     if (w >= workers) {
         return;
     }
-    int64_t x = static_cast<int64_t>(w) * total / workers;
+    const int64_t x0 = static_cast<int64_t>(w) * total / workers;
     const int64_t x_end = static_cast<int64_t>(w + 1) * total / workers;
     int b = uniform(start.row.b);
     int seqlen = uniform(start.row.seqlen);
     int nb = uniform(start.row.n);
-    const int64_t rel = x - static_cast<int64_t>(spr) * uniform(start.row.before);
-    int u = uniform(static_cast<int32_t>(rel / nb));
-    int off = uniform(static_cast<int32_t>(rel - static_cast<int64_t>(u) * nb));
+    int units = stream_units(nb);
+    int64_t row_first = static_cast<int64_t>(spr) * uniform(start.row.before); // first unit of row b
+    int u = uniform(static_cast<int32_t>((x0 - row_first) / units));
+    int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
     uint16_t* lds = lds_tiles[wave];
 
     while (true) {
-        const int seg = static_cast<int>(min(static_cast<int64_t>(nb - off), x_end - x));
-        const int kvh = u / p.head_groups;
-        const int hg = u - kvh * p.head_groups;
-        const int g_first = hg * 16;
-        const int heads_here = min(16, p.group - g_first);
-        const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
-        const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-        const int begin = off * 16;
-        const int end = min((off + seg) * 16, seqlen);
+        // This worker's tiles of stream (b, u): units [x0, x_end) minus the header.
+        const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
+        const int t_hi = static_cast<int>(min(static_cast<int64_t>(nb), x_end - vs - kHeaderTiles));
+        if (t_lo < t_hi) {
+            const int kvh = u / p.head_groups;
+            const int hg = u - kvh * p.head_groups;
+            const int g_first = hg * 16;
+            const int heads_here = min(16, p.group - g_first);
+            const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
+            const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+            const int begin = t_lo * 16;
+            const int end = min(t_hi * 16, seqlen);
 
-        uint4 qop[KS];
-        load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
-        const int win_base = begin >> p.page_shift;
-        const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
+            uint4 qop[KS];
+            load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
+            const int win_base = begin >> p.page_shift;
+            const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
-        f32x4 o[DT];
-        float m;
-        float l;
-        attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds, begin, end, lane, kvh, o, m, l);
-        if (n < heads_here) {
-            if (off == 0 && seg == nb) {
-                write_final<BF16, D>(p, bh_first + n, o, l, j);
-            } else {
-                const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
-                write_partial<D>(p, slot * p.part_heads + n, o, m, l, j);
+            f32x4 o[DT];
+            float m;
+            float l;
+            attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds, begin, end, lane, kvh, o, m, l);
+            if (n < heads_here) {
+                if (t_lo == 0 && t_hi == nb) {
+                    write_final<BF16, D>(p, bh_first + n, o, l, j);
+                } else {
+                    const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
+                    write_partial<D>(p, slot * p.part_heads + n, o, m, l, j);
+                }
             }
         }
-        x += seg;
-        if (x >= x_end) {
+        vs += units;
+        if (vs >= x_end) {
             break;
         }
-        // The stream is exhausted (x < x_end): move to the next stream, past
-        // rows without tokens.
-        off = 0;
+        // Next stream, past rows without tokens (they own no units).
         if (++u == spr) {
             u = 0;
             do {
@@ -539,6 +542,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 seqlen = uniform(min(max(p.seqlens[b], 0), p.row_cap));
             } while (seqlen == 0 && b + 1 < p.batch);
             nb = (seqlen + 15) >> 4;
+            units = stream_units(nb);
         }
     }
 }
