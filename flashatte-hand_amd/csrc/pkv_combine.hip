@@ -133,10 +133,10 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
 
 // Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; its
 // workers w_a .. w_b are found from cache_seqlens with the partition's unit
-// arithmetic (the workers owning the stream's first and last tiles).  One worker means the partition already wrote the row; a row
-// without tokens gets zeros; otherwise the partials in slots w_a + r .. w_b + r
-// are merged: max and weight sum over their LSEs first, then the weighted rows
-// in batches of kBatch loads in flight.
+// arithmetic (the workers owning the stream's first and last tiles).  One
+// worker means the partition already wrote the row; a row without tokens gets
+// zeros; otherwise the partials in slots w_a + r .. w_b + r are merged with
+// their LSEs, kBatch partial rows in flight at a time.
 template <bool BF16, int D>
 __global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
@@ -189,42 +189,66 @@ __global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
     const int64_t lse_stride = p.part_heads;
     const int64_t o_stride = static_cast<int64_t>(p.part_heads) * D;
 
-    float mx = kNegInf;
-    for (int k = lane; k < parts; k += 64) {
+    // One round trip for the common case: the first 64 parts' LSEs (lane k holds
+    // part k) and the first kBatch partial rows are loaded together.
+    const float l0 = lane < parts ? lse[lane * lse_stride] : kNegInf;
+    float x[kBatch][E];
+#pragma unroll
+    for (int v = 0; v < kBatch; ++v) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            x[v][e] = 0.f;
+        }
+        if (v < parts) {
+            load_partial<E>(po + v * o_stride, x[v]);
+        }
+    }
+    float mx = l0;
+    for (int k = lane + 64; k < parts; k += 64) {
         mx = fmaxf(mx, lse[k * lse_stride]);
     }
     mx = group_max<64>(mx);
-    float den = 0.f;
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         acc[e] = 0.f;
     }
-    for (int k0 = 0; k0 < parts; k0 += 64) {
-        // Weight of part k0 + lane; every part has at least one token, so its LSE is finite.
-        const float wl = k0 + lane < parts ? fast_exp2(lse[(k0 + lane) * lse_stride] - mx) : 0.f;
-        den += wl;
-        const int chunk = min(64, parts - k0);
-        for (int c0 = 0; c0 < chunk; c0 += kBatch) {
-            float x[kBatch][E];
+    float wl = lane < parts ? fast_exp2(l0 - mx) : 0.f; // weight of part k0 + lane
+    float den = wl;
 #pragma unroll
-            for (int v = 0; v < kBatch; ++v) {
+    for (int v = 0; v < kBatch; ++v) {
+        const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), v));
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    x[v][e] = 0.f;
-                }
-                if (c0 + v < chunk) {
-                    load_partial<E>(po + (k0 + c0 + v) * o_stride, x[v]);
-                }
+        for (int e = 0; e < E; ++e) {
+            acc[e] = fmaf(wv, x[v][e], acc[e]); // x = 0 past the last part
+        }
+    }
+    // Long rows: the remaining parts, kBatch loads in flight at a time.
+#pragma unroll 1
+    for (int k = kBatch; k < parts; k += kBatch) {
+        if ((k & 63) == 0) {
+            const int kl = k + lane;
+            // Every part has at least one token, so its LSE is finite.
+            wl = kl < parts ? fast_exp2(lse[kl * lse_stride] - mx) : 0.f;
+            den += wl;
+        }
+        float y[kBatch][E];
+#pragma unroll
+        for (int v = 0; v < kBatch; ++v) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                y[v][e] = 0.f;
             }
+            if (k + v < parts) {
+                load_partial<E>(po + (k + v) * o_stride, y[v]);
+            }
+        }
 #pragma unroll
-            for (int v = 0; v < kBatch; ++v) {
-                const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), (c0 + v) & 63));
-                const float wsel = c0 + v < chunk ? wv : 0.f;
+        for (int v = 0; v < kBatch; ++v) {
+            const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), (k + v) & 63));
 #pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    acc[e] = fmaf(wsel, x[v][e], acc[e]);
-                }
+            for (int e = 0; e < E; ++e) {
+                acc[e] = fmaf(wv, y[v][e], acc[e]);
             }
         }
     }
