@@ -14,6 +14,11 @@
 // Largest split count (PKV_MAX_SPLITS in include/pkv_decode.h).
 #define PKV_MAX_SPLITS_DEV 256
 
+// Waves (rows) per workgroup.
+#ifndef PKV_COMBINE_WAVES
+#define PKV_COMBINE_WAVES 4
+#endif
+
 namespace pkv {
 
 __device__ __forceinline__ bool split_nonempty(const CombineParams& p, int seqlen, int s) {
@@ -42,7 +47,7 @@ __device__ __forceinline__ void load_partial(const float* src, float (&x)[E]) {
 // holds split s + 64k).  Weights reach every lane with readlane; partials are
 // folded in with a select, so an unused slot cannot inject NaN.
 template <bool BF16, int D>
-__global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
+__global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_kernel(CombineParams p) {
     constexpr int E = D / 64; // output elements per lane
     constexpr int kBatch = 16;
     constexpr int kLseRegs = (PKV_MAX_SPLITS_DEV + 63) / 64;
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams p) {
 // zeros; otherwise the partials in slots w_a + r .. w_b + r are merged with
 // their LSEs, kBatch partial rows in flight at a time.
 template <bool BF16, int D>
-__global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
+__global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
     constexpr int kBatch = 16;
     const int lane = threadIdx.x & 63;
@@ -262,7 +267,7 @@ __global__ __launch_bounds__(256) void combine_tiles_kernel(CombineParams p) {
 
 template <bool BF16, int D>
 static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    constexpr int kWaves = 4;
+    constexpr int kWaves = PKV_COMBINE_WAVES;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
     if (p.tile_workers > 0) {
         launch_kernel(combine_tiles_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);

@@ -418,6 +418,25 @@ __device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqle
     return r;
 }
 
+// Inclusive prefix sum over the wave's lanes in 32 bits with DPP: Hillis-Steele
+// within each row of 16 lanes (row_shr 1, 2, 4, 8; lanes shifted in from
+// outside the row read 0), then the running totals of rows 0 and 2 are added
+// to rows 1 and 3 (row_bcast:15), and of row 1 to rows 2 and 3 (row_bcast:31).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xf, true));
+}
+
+__device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t x) {
+    x += dpp_u32<0x111, 0xf>(x);
+    x += dpp_u32<0x112, 0xf>(x);
+    x += dpp_u32<0x114, 0xf>(x);
+    x += dpp_u32<0x118, 0xf>(x);
+    x += dpp_u32<0x142, 0xa>(x);
+    x += dpp_u32<0x143, 0xc>(x);
+    return x;
+}
+
 // Inclusive prefix sum over the wave's lanes.
 __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) {
 #pragma unroll
@@ -428,20 +447,56 @@ __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) 
     return x;
 }
 
-// Start of one worker's share: the call's unit count T and the row holding
-// unit x = floor(w T / W).  Rows 0..63 are read once and kept in registers
-// (one load round trip for batches up to 64 rows); larger batches add a sum
-// over the remaining rows and a second, chunked pass to locate the row.
+// Start of one worker's share: the call's unit count T, the clamped worker
+// count W = min(launch workers, T), the share [x0, x_end) with
+// x0 = floor(w T / W), and the row holding unit x0.  Rows 0..63 are read once
+// and kept in registers (one load round trip for batches up to 64 rows);
+// larger batches add a sum over the remaining rows and a second, chunked pass
+// to locate the row.  Batches of up to 64 rows whose unit counts fit 32 bits
+// take a 32-bit path (DPP scan, 32-bit divisions).
 struct WorkerStart {
     int64_t total;
+    int32_t workers;
+    int64_t x0;
+    int64_t x_end;
     RowTiles row;
 };
 
 __device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __restrict__ seqlens, int32_t batch,
                                                            int32_t row_cap, int32_t spr, int32_t w,
-                                                           int32_t workers, int32_t lane) {
+                                                           int32_t launch_workers, int32_t lane) {
     const int32_t sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
     const int32_t n0 = (sl0 + 15) >> 4;
+    WorkerStart ws;
+    // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so 64 rows of
+    // them fit 32 bits when row_cap <= 2^24.
+    if (batch <= 64 && row_cap <= (1 << 24)) {
+        const uint32_t incl = wave_inclusive_scan_u32(static_cast<uint32_t>(stream_units(n0)));
+        const uint32_t rows_total = __builtin_amdgcn_readlane(incl, 63);
+        ws.total = static_cast<int64_t>(spr) * rows_total;
+        ws.workers = static_cast<int32_t>(min(static_cast<int64_t>(launch_workers), ws.total));
+        if (w >= ws.workers) {
+            ws.row.b = -1;
+            return ws;
+        }
+        if (static_cast<uint64_t>(w + 1) * static_cast<uint64_t>(ws.total) < (1ull << 32)) {
+            const uint32_t t32 = static_cast<uint32_t>(ws.total);
+            const uint32_t w32 = static_cast<uint32_t>(ws.workers);
+            ws.x0 = static_cast<uint32_t>(w) * t32 / w32;
+            ws.x_end = static_cast<uint32_t>(w + 1) * t32 / w32;
+        } else {
+            ws.x0 = static_cast<int64_t>(w) * ws.total / ws.workers;
+            ws.x_end = static_cast<int64_t>(w + 1) * ws.total / ws.workers;
+        }
+        const uint32_t y = static_cast<uint32_t>(ws.x0 / spr);
+        const uint64_t hit = __ballot(lane < batch && incl > y);
+        const int32_t l = __builtin_ctzll(hit); // hit != 0: y < rows_total
+        ws.row.b = l;
+        ws.row.seqlen = __shfl(sl0, l, 64);
+        ws.row.n = __shfl(n0, l, 64);
+        ws.row.before = static_cast<int64_t>(__builtin_amdgcn_readlane(incl, l)) - stream_units(ws.row.n);
+        return ws;
+    }
     const int64_t incl0 = wave_inclusive_scan(stream_units(n0), lane);
     int64_t rows_total = __shfl(incl0, 63, 64);
     if (batch > 64) {
@@ -451,14 +506,15 @@ __device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __rest
         }
         rows_total += wave_sum_i64(rest);
     }
-    WorkerStart ws;
     ws.total = static_cast<int64_t>(spr) * rows_total;
-    const int64_t eff = min(static_cast<int64_t>(workers), ws.total);
-    if (w >= eff) {
+    ws.workers = static_cast<int32_t>(min(static_cast<int64_t>(launch_workers), ws.total));
+    if (w >= ws.workers) {
         ws.row.b = -1;
         return ws;
     }
-    const int64_t y = static_cast<int64_t>(w) * ws.total / eff / spr;
+    ws.x0 = static_cast<int64_t>(w) * ws.total / ws.workers;
+    ws.x_end = static_cast<int64_t>(w + 1) * ws.total / ws.workers;
+    const int64_t y = ws.x0 / spr;
     const uint64_t hit = __ballot(lane < batch && incl0 > y);
     if (hit != 0) {
         const int32_t l = __builtin_ctzll(hit);

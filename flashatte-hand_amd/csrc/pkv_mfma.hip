@@ -479,22 +479,23 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         return;
     }
     const int32_t spr = p.num_heads_k * p.head_groups;
+    // Never more workers than units (start.workers): then every worker owns a
+    // unit and the workers owning a stream's tiles are consecutive.
     const WorkerStart start = locate_worker_start(p.seqlens, p.batch, p.row_cap, spr, w, p.tile_workers, lane);
-    const int64_t total = uniform(start.total);
-    // Never more workers than units: then every worker owns a unit and the
-    // workers owning a stream's tiles are consecutive.
-    const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
-    if (w >= workers) {
+    if (w >= uniform(start.workers)) {
         return;
     }
-    const int64_t x0 = static_cast<int64_t>(w) * total / workers;
-    const int64_t x_end = static_cast<int64_t>(w + 1) * total / workers;
+    const int64_t x0 = uniform(start.x0);
+    const int64_t x_end = uniform(start.x_end);
     int b = uniform(start.row.b);
     int seqlen = uniform(start.row.seqlen);
     int nb = uniform(start.row.n);
     int units = stream_units(nb);
     int64_t row_first = static_cast<int64_t>(spr) * uniform(start.row.before); // first unit of row b
-    int u = uniform(static_cast<int32_t>((x0 - row_first) / units));
+    const int64_t into_row = x0 - row_first;
+    int u = uniform(static_cast<int32_t>(into_row < (int64_t{1} << 32)
+                                             ? static_cast<uint32_t>(into_row) / static_cast<uint32_t>(units)
+                                             : into_row / units));
     int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
     uint16_t* lds = lds_tiles[wave];
 
