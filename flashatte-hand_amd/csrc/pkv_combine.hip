@@ -136,12 +136,12 @@ __global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_kernel(Combine
     }
 }
 
-// Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; its
-// workers w_a .. w_b are found from cache_seqlens with the partition's unit
-// arithmetic (the workers owning the stream's first and last tiles).  One
-// worker means the partition already wrote the row; a row without tokens gets
-// zeros; otherwise the partials in slots w_a + r .. w_b + r are merged with
-// their LSEs, kBatch partial rows in flight at a time.
+// Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; the
+// workers w_a .. w_b owning its tiles are found from cache_seqlens with the
+// partition's unit arithmetic.  One worker means the partition already wrote
+// the row; a row without tokens gets zeros; otherwise the partials in slots
+// w_a + r .. w_b + r are merged with their LSEs, kBatch partial rows in flight
+// at a time.
 template <bool BF16, int D>
 __global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
@@ -181,9 +181,9 @@ __global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_tiles_kernel(C
     // Unit of the stream's first tile.
     const int64_t first =
         static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
-    const int32_t workers = static_cast<int32_t>(min(static_cast<int64_t>(p.tile_workers), total));
-    const int32_t wa = tile_worker_of(first, total, workers);
-    const int32_t wb = tile_worker_of(first + nb - 1, total, workers);
+    const TilePlan plan = make_tile_plan(total, p.tile_workers);
+    const int32_t wa = tile_worker_of(first, plan.total, plan.workers);
+    const int32_t wb = tile_worker_of(first + nb - 1, plan.total, plan.workers);
     if (wa == wb) {
         return;
     }

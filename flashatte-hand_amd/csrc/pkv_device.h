@@ -38,7 +38,7 @@ struct PartitionParams {
     int32_t num_items;    // splits * B * Hk * head_groups
     int32_t num_groups;   // workgroups in the grid (a multiple of 8)
     int32_t split_fastest; // item order: 1 = split index fastest, 0 = (kv head, head group) fastest
-    int32_t tile_workers; // > 0: tile-balanced schedule with this many waves (see TileSchedule)
+    int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
     int32_t part_heads;   // heads per partial slot in the tile-balanced schedule
     float scale_log2;     // softmax_scale * log2(e)
 };
@@ -447,86 +447,80 @@ __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) 
     return x;
 }
 
-// Start of one worker's share: the call's unit count T, the clamped worker
-// count W = min(launch workers, T), the share [x0, x_end) with
-// x0 = floor(w T / W), and the row holding unit x0.  Rows 0..63 are read once
-// and kept in registers (one load round trip for batches up to 64 rows);
-// larger batches add a sum over the remaining rows and a second, chunked pass
-// to locate the row.  Batches of up to 64 rows whose unit counts fit 32 bits
-// take a 32-bit path (DPP scan, 32-bit divisions).
-struct WorkerStart {
-    int64_t total;
-    int32_t workers;
-    int64_t x0;
-    int64_t x_end;
-    RowTiles row;
+// Units per row of the call, as a wave-wide prefix.  Rows 0..63 are read once
+// and kept in registers; larger batches add a sum over the remaining rows, and
+// locating a unit in them takes a chunked pass (locate_row).  Batches of up to
+// 64 rows whose unit counts fit 32 bits use a 32-bit DPP scan.
+struct RowScan {
+    int64_t rows_total; // sum over rows of stream_units(n_b)
+    bool fast;          // incl holds the whole prefix (batch <= 64, 32-bit)
+    uint32_t incl;      // lane b: sum of stream_units(n_b') for b' <= b (fast path)
+    int32_t sl0;        // lane b: clamped seqlen of row b (b < 64)
+    int32_t n0;         // lane b: tiles of row b
 };
 
-__device__ __forceinline__ WorkerStart locate_worker_start(const int32_t* __restrict__ seqlens, int32_t batch,
-                                                           int32_t row_cap, int32_t spr, int32_t w,
-                                                           int32_t launch_workers, int32_t lane) {
-    const int32_t sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
-    const int32_t n0 = (sl0 + 15) >> 4;
-    WorkerStart ws;
+__device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens, int32_t batch, int32_t row_cap,
+                                             int32_t lane) {
+    RowScan rs;
+    rs.sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
+    rs.n0 = (rs.sl0 + 15) >> 4;
     // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so 64 rows of
     // them fit 32 bits when row_cap <= 2^24.
-    if (batch <= 64 && row_cap <= (1 << 24)) {
-        const uint32_t incl = wave_inclusive_scan_u32(static_cast<uint32_t>(stream_units(n0)));
-        const uint32_t rows_total = __builtin_amdgcn_readlane(incl, 63);
-        ws.total = static_cast<int64_t>(spr) * rows_total;
-        ws.workers = static_cast<int32_t>(min(static_cast<int64_t>(launch_workers), ws.total));
-        if (w >= ws.workers) {
-            ws.row.b = -1;
-            return ws;
-        }
-        if (static_cast<uint64_t>(w + 1) * static_cast<uint64_t>(ws.total) < (1ull << 32)) {
-            const uint32_t t32 = static_cast<uint32_t>(ws.total);
-            const uint32_t w32 = static_cast<uint32_t>(ws.workers);
-            ws.x0 = static_cast<uint32_t>(w) * t32 / w32;
-            ws.x_end = static_cast<uint32_t>(w + 1) * t32 / w32;
-        } else {
-            ws.x0 = static_cast<int64_t>(w) * ws.total / ws.workers;
-            ws.x_end = static_cast<int64_t>(w + 1) * ws.total / ws.workers;
-        }
-        const uint32_t y = static_cast<uint32_t>(ws.x0 / spr);
-        const uint64_t hit = __ballot(lane < batch && incl > y);
-        const int32_t l = __builtin_ctzll(hit); // hit != 0: y < rows_total
-        ws.row.b = l;
-        ws.row.seqlen = __shfl(sl0, l, 64);
-        ws.row.n = __shfl(n0, l, 64);
-        ws.row.before = static_cast<int64_t>(__builtin_amdgcn_readlane(incl, l)) - stream_units(ws.row.n);
-        return ws;
+    rs.fast = batch <= 64 && row_cap <= (1 << 24);
+    if (rs.fast) {
+        rs.incl = wave_inclusive_scan_u32(static_cast<uint32_t>(stream_units(rs.n0)));
+        rs.rows_total = __builtin_amdgcn_readlane(rs.incl, 63);
+        return rs;
     }
-    const int64_t incl0 = wave_inclusive_scan(stream_units(n0), lane);
-    int64_t rows_total = __shfl(incl0, 63, 64);
-    if (batch > 64) {
-        int64_t rest = 0;
-        for (int32_t b = lane + 64; b < batch; b += 64) {
-            rest += stream_units(row_tiles(seqlens, b, row_cap));
-        }
-        rows_total += wave_sum_i64(rest);
+    rs.incl = 0;
+    int64_t sum = stream_units(rs.n0);
+    for (int32_t b = lane + 64; b < batch; b += 64) {
+        sum += stream_units(row_tiles(seqlens, b, row_cap));
     }
-    ws.total = static_cast<int64_t>(spr) * rows_total;
-    ws.workers = static_cast<int32_t>(min(static_cast<int64_t>(launch_workers), ws.total));
-    if (w >= ws.workers) {
-        ws.row.b = -1;
-        return ws;
-    }
-    ws.x0 = static_cast<int64_t>(w) * ws.total / ws.workers;
-    ws.x_end = static_cast<int64_t>(w + 1) * ws.total / ws.workers;
-    const int64_t y = ws.x0 / spr;
-    const uint64_t hit = __ballot(lane < batch && incl0 > y);
-    if (hit != 0) {
-        const int32_t l = __builtin_ctzll(hit);
-        ws.row.b = l;
-        ws.row.seqlen = __shfl(sl0, l, 64);
-        ws.row.n = __shfl(n0, l, 64);
-        ws.row.before = __shfl(incl0, l, 64) - stream_units(ws.row.n);
-    } else {
-        ws.row = locate_row(seqlens, batch, row_cap, y, lane);
-    }
-    return ws;
+    rs.rows_total = wave_sum_i64(sum);
+    return rs;
 }
+
+// Row holding stream-unit index y (0 <= y < rows_total).
+__device__ __forceinline__ RowTiles locate_unit_row(const RowScan& rs, const int32_t* __restrict__ seqlens,
+                                                    int32_t batch, int32_t row_cap, int64_t y, int32_t lane) {
+    if (rs.fast) {
+        const uint64_t hit = __ballot(lane < batch && rs.incl > static_cast<uint32_t>(y));
+        const int32_t l = __builtin_ctzll(hit); // hit != 0 for y < rows_total
+        RowTiles r;
+        r.b = l;
+        r.seqlen = __shfl(rs.sl0, l, 64);
+        r.n = __shfl(rs.n0, l, 64);
+        r.before = static_cast<int64_t>(__builtin_amdgcn_readlane(rs.incl, l)) - stream_units(r.n);
+        return r;
+    }
+    return locate_row(seqlens, batch, row_cap, y, lane);
+}
+
+// floor(a * b / c) for a, b >= 0, c > 0, a * b < 2^63; 32-bit when it fits.
+__device__ __forceinline__ int64_t muldiv(int64_t a, int64_t b, int64_t c) {
+    const uint64_t ab = static_cast<uint64_t>(a) * static_cast<uint64_t>(b);
+    if (ab < (1ull << 32) && c < (int64_t{1} << 32)) {
+        return static_cast<uint32_t>(ab) / static_cast<uint32_t>(c);
+    }
+    return static_cast<int64_t>(ab / static_cast<uint64_t>(c));
+}
+
+// Shares of the tile-balanced schedule: worker w of W = min(launched workers,
+// T) takes units [floor(w T / W), floor((w + 1) T / W)).
+struct TilePlan {
+    int64_t total;   // T: units of the call
+    int32_t workers; // W
+};
+
+__device__ __forceinline__ TilePlan make_tile_plan(int64_t total, int32_t launch_workers) {
+    TilePlan pl;
+    pl.total = total;
+    pl.workers = static_cast<int32_t>(min(static_cast<int64_t>(launch_workers), total));
+    return pl;
+}
+
+__device__ __forceinline__ int64_t share_start(int64_t w, const TilePlan& pl) { return muldiv(w, pl.total, pl.workers); }
 
 __device__ __forceinline__ int32_t uniform(int32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 __device__ __forceinline__ int64_t uniform(int64_t x) {

@@ -457,13 +457,12 @@ void partition_mfma_kernel(PartitionParams p) {
     }
 }
 
-// Tile-balanced schedule: wave w of p.tile_workers streams tiles
-// [floor(w T / W), floor((w + 1) T / W)) of the call's tile sequence (streams
-// and slots as defined with row_tiles in pkv_device.h), segment by segment.  A segment that is a
-// whole stream is written to the output; any other leaves a partial in slot
-// w + r.  The workgroup's LDS request is padded on the host so that one
-// workgroup occupies a CU: the dispatcher then spreads the grid over all CUs
-// instead of doubling some up while others idle.
+// Tile-balanced schedule (streams, units, shares and slots as defined with
+// row_tiles and make_tile_plan in pkv_device.h): wave w streams its share,
+// segment by segment.  A segment that is a whole stream is written to the
+// output; any other leaves a partial in slot w + r for the combine.  The workgroup's LDS request is padded on the
+// host so that one workgroup occupies a CU: the dispatcher then spreads the
+// grid over all CUs instead of doubling some up while others idle.
 template <bool BF16, int D, bool WIDE, int DEPTH, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
     constexpr int KS = D / 32;
@@ -479,73 +478,75 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         return;
     }
     const int32_t spr = p.num_heads_k * p.head_groups;
-    // Never more workers than units (start.workers): then every worker owns a
-    // unit and the workers owning a stream's tiles are consecutive.
-    const WorkerStart start = locate_worker_start(p.seqlens, p.batch, p.row_cap, spr, w, p.tile_workers, lane);
-    if (w >= uniform(start.workers)) {
+    const RowScan scan = scan_rows(p.seqlens, p.batch, p.row_cap, lane);
+    const TilePlan plan = make_tile_plan(static_cast<int64_t>(spr) * uniform(scan.rows_total), p.tile_workers);
+    if (w >= plan.workers) {
         return;
     }
-    const int64_t x0 = uniform(start.x0);
-    const int64_t x_end = uniform(start.x_end);
-    int b = uniform(start.row.b);
-    int seqlen = uniform(start.row.seqlen);
-    int nb = uniform(start.row.n);
-    int units = stream_units(nb);
-    int64_t row_first = static_cast<int64_t>(spr) * uniform(start.row.before); // first unit of row b
-    const int64_t into_row = x0 - row_first;
-    int u = uniform(static_cast<int32_t>(into_row < (int64_t{1} << 32)
-                                             ? static_cast<uint32_t>(into_row) / static_cast<uint32_t>(units)
-                                             : into_row / units));
-    int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
     uint16_t* lds = lds_tiles[wave];
 
-    while (true) {
-        // This worker's tiles of stream (b, u): units [x0, x_end) minus the header.
-        const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
-        const int t_hi = static_cast<int>(min(static_cast<int64_t>(nb), x_end - vs - kHeaderTiles));
-        if (t_lo < t_hi) {
-            const int kvh = u / p.head_groups;
-            const int hg = u - kvh * p.head_groups;
-            const int g_first = hg * 16;
-            const int heads_here = min(16, p.group - g_first);
-            const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
-            const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-            const int begin = t_lo * 16;
-            const int end = min(t_hi * 16, seqlen);
+    // Streams the tiles among this worker's units [x0, x_end), stream by
+    // stream; partials go to slot w + r.
+    auto run_share = [&](int64_t x0, int64_t x_end) {
+        const RowTiles rt = locate_unit_row(scan, p.seqlens, p.batch, p.row_cap, muldiv(x0, 1, spr), lane);
+        int b = uniform(rt.b);
+        int seqlen = uniform(rt.seqlen);
+        int nb = uniform(rt.n);
+        int units = stream_units(nb);
+        const int64_t row_first = static_cast<int64_t>(spr) * uniform(rt.before); // first unit of row b
+        int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));
+        int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
+        while (true) {
+            // The share's tiles of stream (b, u): units [x0, x_end) minus the header.
+            const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
+            const int t_hi = static_cast<int>(min(static_cast<int64_t>(nb), x_end - vs - kHeaderTiles));
+            if (t_lo < t_hi) {
+                const int kvh = u / p.head_groups;
+                const int hg = u - kvh * p.head_groups;
+                const int g_first = hg * 16;
+                const int heads_here = min(16, p.group - g_first);
+                const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
+                const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
+                const int begin = t_lo * 16;
+                const int end = min(t_hi * 16, seqlen);
 
-            uint4 qop[KS];
-            load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
-            const int win_base = begin >> p.page_shift;
-            const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
+                uint4 qop[KS];
+                load_q_operand<D>(p, bh_first, heads_here, n, j, qop);
+                const int win_base = begin >> p.page_shift;
+                const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
-            f32x4 o[DT];
-            float m;
-            float l;
-            attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds, begin, end, lane, kvh, o, m, l);
-            if (n < heads_here) {
-                if (t_lo == 0 && t_hi == nb) {
-                    write_final<BF16, D>(p, bh_first + n, o, l, j);
-                } else {
-                    const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
-                    write_partial<D>(p, slot * p.part_heads + n, o, m, l, j);
+                f32x4 o[DT];
+                float m;
+                float l;
+                attend_range<BF16, D, WIDE, DEPTH>(p, bt_row, win, win_base, qop, lds, begin, end, lane, kvh, o, m,
+                                                   l);
+                if (n < heads_here) {
+                    if (t_lo == 0 && t_hi == nb) {
+                        write_final<BF16, D>(p, bh_first + n, o, l, j);
+                    } else {
+                        const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
+                        write_partial<D>(p, slot * p.part_heads + n, o, m, l, j);
+                    }
                 }
             }
+            vs += units;
+            if (vs >= x_end) {
+                break;
+            }
+            // Next stream, past rows without tokens (they own no units).
+            if (++u == spr) {
+                u = 0;
+                do {
+                    ++b;
+                    seqlen = uniform(min(max(p.seqlens[b], 0), p.row_cap));
+                } while (seqlen == 0 && b + 1 < p.batch);
+                nb = (seqlen + 15) >> 4;
+                units = stream_units(nb);
+            }
         }
-        vs += units;
-        if (vs >= x_end) {
-            break;
-        }
-        // Next stream, past rows without tokens (they own no units).
-        if (++u == spr) {
-            u = 0;
-            do {
-                ++b;
-                seqlen = uniform(min(max(p.seqlens[b], 0), p.row_cap));
-            } while (seqlen == 0 && b + 1 < p.batch);
-            nb = (seqlen + 15) >> 4;
-            units = stream_units(nb);
-        }
-    }
+    };
+
+    run_share(share_start(w, plan), share_start(w + 1, plan));
 }
 
 // Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
