@@ -1,26 +1,24 @@
-// pkv_mfma.hip — MFMA partition kernel for paged-KV GQA decode on gfx950.
+// pkv_mfma.hip — MFMA partition kernels for paged-KV GQA decode on gfx950.
 //
-// One wave64 owns one work item (b, kv head, group of up to 16 query heads,
-// split) and walks its token range in tiles of 16 tokens.  Lane l is
-// (n = l & 15, j = l >> 4).
+// One wave64 works on one head slice (one kv head, up to 16 of its query
+// heads, zero-padded) over a token range, in tiles of 16 tokens.  Lane l is
+// (n = l & 15, j = l >> 4).  Per tile:
 //
+//   load   K and V rows in row layout (D/8 lanes per token, whole 128-byte
+//          lines, nontemporal 16-byte loads), page ids from a register window;
+//   stage  the rows into the wave's LDS tiles, then issue the next tile's
+//          loads into the freed registers (one tile in flight during compute);
 //   S^T[16 tok x 16 heads] = K[16 tok x D] . Q^T[D x 16 heads]
-//       v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps.  A = K: lane loads token n,
-//       dims 8(4kk + j) .. +7 straight from HBM (16 B/lane, 64 contiguous bytes
-//       per token per step).  B = Q^T: head n, same dims, held in VGPRs for the
-//       whole item (heads beyond the group are zero columns).
-//       Result: lane holds head n, tokens 4j + i (i = 0..3).
-//   softmax: fp32, log2 domain, one max/rescale per tile; the 4 scores a lane
-//       holds become the B operand of PV after one 16-bit pack (p <= 1).
+//          v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps.  A = K read back from
+//          LDS (lane: token n, dims 8(4kk + j) .. +7); B = Q^T held in VGPRs.
+//          Result: lane holds head n, tokens 4j + i (i = 0..3);
+//   softmax fp32, log2 domain, one max per tile, lazy rescale (p <= 2^8); the
+//          4 probabilities a lane holds become the B operand of PV after one
+//          16-bit pack;
 //   O^T[D x 16 heads] += V^T[D x 16 tok] . P^T[16 tok x 16 heads]
-//       v_mfma_f32_16x16x16{bf16_1k,f16}, D/16 output tiles.  A = V^T needs
-//       4 tokens of one dim per lane, so the V tile (loaded with the same
-//       addresses as K) is written to a per-wave LDS tile with rows padded by
-//       16 bytes, which spreads both the row writes and the column gathers
-//       over distinct banks.
-//   The next tile's K and V are loaded into a second register set before the
-//   current tile is computed.
-// The per-wave LDS tile is private to the wave and LDS operations of a wave
+//          v_mfma_f32_16x16x16{bf16_1k,f16}, D/16 output tiles; A = V^T from
+//          the LDS V tile through ds_read_b64_tr_b16.
+// The per-wave LDS tiles are private to the wave and LDS operations of a wave
 // complete in order, so no barrier is needed.
 //
 // Reference semantics followed: submission-oj/best_flashattn_kvcache_decode.cu
@@ -121,15 +119,15 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams&
     }
 }
 
-// LDS tiles of one wave: 16 token rows of K and of V, each row padded by 16
-// bytes (row stride 2D + 16 bytes).  The padding shifts consecutive rows by 16
-// bytes across the banks, so the row writes, the K operand reads (16 rows,
-// same chunk) and the V column gathers (4 rows x 32 contiguous bytes) are
-// spread over distinct banks, and every address is a per-lane base plus an
-// immediate offset.
+// LDS tiles of one wave: 16 token rows of K and of V, each row padded by 32
+// bytes (row stride 2D + 32 bytes).  Measured with SQ_LDS_BANK_CONFLICT on
+// gfx950: with 16-byte padding the V transpose reads spent half their cycles
+// in bank conflicts (a quarter of the kernel's LDS cycles); with 32 bytes the
+// kernel has none, and the row writes are conflict-free with any padding.
+// Every address is a per-lane base plus an immediate offset.
 template <int D>
 struct VTile {
-    static constexpr int kRow = D + 8; // row stride in 16-bit elements
+    static constexpr int kRow = D + 16; // row stride in 16-bit elements
     static constexpr int kElems = 16 * kRow;
 };
 
