@@ -337,16 +337,7 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     p.row_cap = static_cast<int32_t>(std::min<int64_t>(desc->block_table_stride * r.P, INT32_MAX));
     p.batch = static_cast<int32_t>(r.B);
     p.num_items = static_cast<int32_t>(items);
-    // With strided wave->item mapping, a multiple of 8 workgroups so each XCD
-    // owns the items with index = XCD mod 8 (see decode_item).
-    {
-        const int64_t groups = (items + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup;
-        p.num_groups = static_cast<int32_t>(PKV_STRIDED_ITEMS ? round_up(groups, 8) : groups);
-    }
-#ifndef PKV_ITEM_ORDER
-#define PKV_ITEM_ORDER 1
-#endif
-    p.split_fastest = PKV_ITEM_ORDER == 1 ? 0 : PKV_ITEM_ORDER == 2 ? 1 : ((r.Hk * r.head_groups) % 8 == 0 ? 0 : 1);
+    p.num_groups = static_cast<int32_t>((items + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup);
     p.tile_workers = tiles ? plan.splits : 0;
     p.part_heads = static_cast<int32_t>(part_heads(r));
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;

@@ -14,12 +14,10 @@
 // Largest split count (PKV_MAX_SPLITS in include/pkv_decode.h).
 #define PKV_MAX_SPLITS_DEV 256
 
-// Waves (rows) per workgroup.
-#ifndef PKV_COMBINE_WAVES
-#define PKV_COMBINE_WAVES 4
-#endif
-
 namespace pkv {
+
+// Waves (rows) per workgroup; 2, 8 and 16 measured the same.
+constexpr int kCombineWaves = 4;
 
 __device__ __forceinline__ bool split_nonempty(const CombineParams& p, int seqlen, int s) {
     const TokenRange r = split_tokens_of(seqlen, p.page_shift, s, p.splits, p.split_tokens);
@@ -47,7 +45,7 @@ __device__ __forceinline__ void load_partial(const float* src, float (&x)[E]) {
 // holds split s + 64k).  Weights reach every lane with readlane; partials are
 // folded in with a select, so an unused slot cannot inject NaN.
 template <bool BF16, int D>
-__global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_kernel(CombineParams p) {
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(CombineParams p) {
     constexpr int E = D / 64; // output elements per lane
     constexpr int kBatch = 16;
     constexpr int kLseRegs = (PKV_MAX_SPLITS_DEV + 63) / 64;
@@ -143,7 +141,7 @@ __global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_kernel(Combine
 // w_a + r .. w_b + r are merged with their LSEs, kBatch partial rows in flight
 // at a time.
 template <bool BF16, int D>
-__global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_tiles_kernel(CombineParams p) {
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
     constexpr int kBatch = 16;
     const int lane = threadIdx.x & 63;
@@ -267,7 +265,7 @@ __global__ __launch_bounds__(64 * PKV_COMBINE_WAVES) void combine_tiles_kernel(C
 
 template <bool BF16, int D>
 static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    constexpr int kWaves = PKV_COMBINE_WAVES;
+    constexpr int kWaves = kCombineWaves;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
     if (p.tile_workers > 0) {
         launch_kernel(combine_tiles_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);

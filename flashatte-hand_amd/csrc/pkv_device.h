@@ -36,8 +36,7 @@ struct PartitionParams {
     int32_t row_cap;      // tokens a block_table row can address (bt_stride * P, clamped)
     int32_t batch;        // B
     int32_t num_items;    // splits * B * Hk * head_groups
-    int32_t num_groups;   // workgroups in the grid (a multiple of 8)
-    int32_t split_fastest; // item order: 1 = split index fastest, 0 = (kv head, head group) fastest
+    int32_t num_groups;   // workgroups in the grid
     int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
     int32_t part_heads;   // heads per partial slot in the tile-balanced schedule
     float scale_log2;     // softmax_scale * log2(e)
@@ -263,13 +262,9 @@ __device__ __forceinline__ TokenRange split_tokens_of(int32_t seqlen, int32_t pa
     return r;
 }
 
-// Work items and the 8 XCDs.  Workgroups are dealt to the XCDs round-robin
-// (workgroup w runs on XCD w % 8), so wave k of workgroup w takes item
-// k * num_groups + w: with num_groups a multiple of 8, XCD x owns exactly the
-// items whose index is x mod 8.  The item index puts a dimension that every
-// row has equally many of fastest — the (kv head, head group) unit when there
-// are a multiple of 8 of them, else the split window — so each XCD gets the
-// same share of every row and ragged rows cannot overload one XCD.
+// Work items of the split schedules: item = (split * B + b) * units + u with
+// u = kv head * head_groups + head group, so consecutive waves (and
+// workgroups) take the (kv head, head group) units of one row and one split.
 struct Item {
     int32_t split;
     int32_t b;
@@ -277,48 +272,31 @@ struct Item {
     int32_t hg;
 };
 
-#ifndef PKV_WAVES_PER_GROUP
-#define PKV_WAVES_PER_GROUP 4
-#endif
-#ifndef PKV_STRIDED_ITEMS
-#define PKV_STRIDED_ITEMS 0
-#endif
-constexpr int kWavesPerGroup = PKV_WAVES_PER_GROUP;
+// Waves per workgroup of the split-schedule kernels.
+constexpr int kWavesPerGroup = 4;
 
 // Compute units of gfx950 (MI355X): grids are sized against it.
 constexpr int kComputeUnits = 256;
 
 // Waves per workgroup (= per CU) of the tile-balanced partition kernel.
 // Measured on MI355X over the five workload shapes: 4 (one per SIMD) streams
-// faster than 2, 3 or 8, and than 4 with two tiles of prefetch per wave.
+// faster than 2, 3, 5, 6 or 8, and than 4 with two tiles of prefetch per wave.
 #ifndef PKV_TILE_WAVES
 #define PKV_TILE_WAVES 4
 #endif
 constexpr int kTileWaves = PKV_TILE_WAVES;
 
-__device__ __forceinline__ int32_t wave_item(const PartitionParams& p) {
-    const int32_t wave = static_cast<int32_t>(threadIdx.x >> 6);
-    if (PKV_STRIDED_ITEMS) {
-        return wave * p.num_groups + static_cast<int32_t>(blockIdx.x);
-    }
-    return static_cast<int32_t>(blockIdx.x) * kWavesPerGroup + wave;
+__device__ __forceinline__ int32_t wave_item() {
+    return static_cast<int32_t>(blockIdx.x) * kWavesPerGroup + static_cast<int32_t>(threadIdx.x >> 6);
 }
 
 __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams& p) {
     const int32_t units = p.num_heads_k * p.head_groups;
     Item it;
-    int32_t u;
-    if (p.split_fastest) {
-        it.split = item % p.splits;
-        const int32_t rest = item / p.splits;
-        u = rest % units;
-        it.b = rest / units;
-    } else {
-        u = item % units;
-        const int32_t rest = item / units;
-        it.b = rest % p.batch;
-        it.split = rest / p.batch;
-    }
+    const int32_t u = item % units;
+    const int32_t rest = item / units;
+    it.b = rest % p.batch;
+    it.split = rest / p.batch;
     it.kvh = u / p.head_groups;
     it.hg = u - it.kvh * p.head_groups;
     return it;

@@ -368,14 +368,10 @@ __device__ __forceinline__ void write_partial(const PartitionParams& p, int64_t 
     }
 }
 
-#ifndef PKV_MFMA_WAVES_PER_EU
-#define PKV_MFMA_WAVES_PER_EU 1
-#endif
-
 // Split schedules (one split, page-balanced splits, token windows): one wave
 // per work item (b, kv head, head group, split).
 template <bool BF16, int D, bool WIDE, int DEPTH>
-__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(PKV_MFMA_WAVES_PER_EU)))
+__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
 void partition_mfma_kernel(PartitionParams p) {
     constexpr int KS = D / 32;
     constexpr int DT = D / 16;
@@ -385,7 +381,7 @@ void partition_mfma_kernel(PartitionParams p) {
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int item = wave_item(p);
+    const int item = wave_item();
     if (item >= p.num_items) {
         return;
     }
@@ -555,10 +551,6 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
 #endif
 constexpr int kSplitDepthFewItems = 2;
 
-#ifndef PKV_TILE_ONE_GROUP_PER_CU
-#define PKV_TILE_ONE_GROUP_PER_CU 1
-#endif
-
 template <bool BF16, int D, bool WIDE>
 static void launch_tiles_t(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = kTileWaves;
@@ -567,7 +559,7 @@ static void launch_tiles_t(const PartitionParams& p, hipStream_t stream, const L
     // workgroup per CU.
     constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
     constexpr size_t kHalf = 80 * 1024;
-    const size_t dyn = PKV_TILE_ONE_GROUP_PER_CU && kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
+    const size_t dyn = kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
     launch_kernel(partition_tiles_kernel<BF16, D, WIDE, PKV_MFMA_DEPTH, kWaves>, dim3(blocks), dim3(64 * kWaves), dyn,
                   stream, ev, p);
 }

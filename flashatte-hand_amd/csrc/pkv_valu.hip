@@ -28,7 +28,7 @@ __global__ __launch_bounds__(64 * kWavesPerGroup) void partition_valu_kernel(Par
     static_assert(L * R == 64, "head_dim must be 64, 128, 256 or 512");
 
     const int lane = threadIdx.x & 63;
-    const int item = wave_item(p);
+    const int item = wave_item();
     if (item >= p.num_items) {
         return;
     }
