@@ -19,18 +19,9 @@
 
 namespace {
 
-// gfx950 (MI355X) compute units; the split heuristics size grids against it.
+// gfx950 (MI355X) compute units; the tile-balanced schedule sizes its grid against it.
 constexpr int kComputeUnits = pkv::kComputeUnits;
 
-// Split-window heuristic (tokens).  Measured on MI355X over the five
-// workload shapes: windows of 512 tokens beat shorter ones (each work item pays
-// a prologue of dependent loads and writes a partial), while the split count
-// per row is kept <= 64 because the combine's cost grows with it.
-constexpr int kBaseSplitTokens = 512;
-constexpr int kMinSplitTokens = 256;
-constexpr int kMaxSplitsPerRow = 64;
-// Below this many work items (4 per CU) the GPU is under-filled: shorten the window.
-constexpr int kMinItems = 4 * kComputeUnits;
 // Tile-balanced schedule: one workgroup of pkv::kTileWaves waves per CU, and
 // no fewer than this many 16-token tiles per wave (each wave's share starts
 // with a few dependent loads that more tiles amortise).
@@ -55,12 +46,12 @@ int ilog2(int64_t x) {
     return s;
 }
 
+// VALU math keeps every head's q in registers: at most 4 heads per wave; larger
+// groups are split into head groups of 4 (each re-reads the K/V rows).
 int valu_heads_per_wave(int64_t group) {
     if (group <= 1) return 1;
     if (group <= 2) return 2;
-    if (group <= 4) return 4;
-    if (group <= 8) return 8;
-    return 16;
+    return 4;
 }
 
 // Kernel family per shape.  Chosen from measurements on MI355X (bench.py
@@ -132,24 +123,6 @@ int64_t effective_max_seqlen(const pkv_decode_desc* d, const Resolved& r) {
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-// Window length for the heuristic: kBaseSplitTokens, lengthened (powers of
-// two) until the longest row has at most kMaxSplitsPerRow windows, then halved
-// (down to kMinSplitTokens) while fewer than kMinItems work items would exist.
-// Unlike the reference's (B, seqlen_k) table (best_flashattn_kvcache_decode.cu:1039-1076)
-// it counts KV heads and head groups, and equal windows keep ragged rows from
-// leaving a long tail of oversized items.
-int64_t choose_split_tokens(const Resolved& r, int64_t max_seqlen) {
-    const int64_t units = r.B * r.Hk * r.head_groups;
-    int64_t tok = kBaseSplitTokens;
-    while ((max_seqlen + tok - 1) / tok > kMaxSplitsPerRow) {
-        tok *= 2;
-    }
-    while (tok > kMinSplitTokens && units * ((max_seqlen + tok - 1) / tok) < kMinItems) {
-        tok /= 2;
-    }
-    return tok;
-}
-
 // Streams of the tile-balanced schedule per row: (kv head, head group) pairs.
 int64_t streams_per_row(const Resolved& r) { return r.Hk * r.head_groups; }
 
@@ -172,10 +145,10 @@ SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_sp
     }
     const int64_t max_seqlen = effective_max_seqlen(d, r);
     if (num_splits == 0) {
-        if (d->split_tokens == 0 && r.path == PKV_PATH_MFMA) {
+        if (d->split_tokens == 0) {
             return {PKV_SCHED_TILES, tile_workers(r, max_seqlen), 0};
         }
-        int64_t tok = d->split_tokens > 0 ? d->split_tokens : choose_split_tokens(r, max_seqlen);
+        int64_t tok = d->split_tokens;
         int64_t s = (max_seqlen + tok - 1) / tok;
         if (s > PKV_MAX_SPLITS) {
             tok = round_up((max_seqlen + PKV_MAX_SPLITS - 1) / PKV_MAX_SPLITS, 16);
@@ -352,10 +325,8 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         comb_ev = {ev[2], ev[3]};
     }
 
-    const hipError_t e = r.path == PKV_PATH_MFMA
-                             ? pkv::launch_partition_mfma(p, bf16, static_cast<int>(r.D), s, part_ev)
-                             : pkv::launch_partition_valu(p, bf16, static_cast<int>(r.D), r.heads_per_wave, s,
-                                                          part_ev);
+    const hipError_t e = pkv::launch_partition(p, r.path == PKV_PATH_MFMA, bf16, static_cast<int>(r.D),
+                                               r.heads_per_wave, s, part_ev);
     if (e != hipSuccess) {
         return PKV_ELAUNCH;
     }
@@ -376,6 +347,7 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         c.batch = p.batch;
         c.group = p.group;
         c.head_groups = p.head_groups;
+        c.heads_per_wave = r.heads_per_wave;
         if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s, comb_ev) != hipSuccess) {
             return PKV_ELAUNCH;
         }

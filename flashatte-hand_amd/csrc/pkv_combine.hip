@@ -153,8 +153,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     const int h = row - b * p.num_heads;
     const int kvh = h / p.group;
     const int g = h - kvh * p.group;
-    const int hg = g / 16;
-    const int hn = g - 16 * hg;
+    const int hg = g / p.heads_per_wave;
+    const int hn = g - p.heads_per_wave * hg;
     const int spr = (p.num_heads / p.group) * p.head_groups;
     const int u = kvh * p.head_groups + hg;
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;

@@ -60,6 +60,7 @@ struct CombineParams {
     int32_t batch;
     int32_t group;        // H / Hk
     int32_t head_groups;  // streams per (b, kv head)
+    int32_t heads_per_wave; // query heads per stream (16 MFMA, 1/2/4 VALU)
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();

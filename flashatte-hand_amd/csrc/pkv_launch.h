@@ -28,13 +28,12 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_
     }
 }
 
-// VALU partition kernel; heads_per_wave in {1, 2, 4, 8, 16}, head_dim in {64, 128, 256}.
-hipError_t launch_partition_valu(const PartitionParams& p, bool bf16, int head_dim, int heads_per_wave,
-                                 hipStream_t stream, const LaunchEvents& ev);
-
-// MFMA partition kernel; 16 heads per wave (zero-padded), head_dim in {64, 128, 256}.
-hipError_t launch_partition_mfma(const PartitionParams& p, bool bf16, int head_dim, hipStream_t stream,
-                                 const LaunchEvents& ev);
+// Partition kernels (pkv_partition.hip): MFMA math (16 heads per wave,
+// zero-padded) or VALU math (heads_per_wave in {1, 2, 4}); head_dim in
+// {64, 128, 256}; the tile-balanced kernel when p.tile_workers > 0, else the
+// split-schedule kernel.
+hipError_t launch_partition(const PartitionParams& p, bool mfma, bool bf16, int head_dim, int heads_per_wave,
+                            hipStream_t stream, const LaunchEvents& ev);
 
 // LSE combine of split partials into the 16-bit output.
 hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,

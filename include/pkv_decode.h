@@ -40,8 +40,8 @@ extern "C" {
 
 /* Kernel family selector (pkv_decode_desc.path). */
 #define PKV_PATH_AUTO 0        /* measured choice per shape */
-#define PKV_PATH_VALU 1        /* VALU dot2 products + DPP row reductions */
-#define PKV_PATH_MFMA 2        /* gfx950 16x16x32 / 16x16x16 MFMA for QK^T and PV */
+#define PKV_PATH_VALU 1        /* VALU dot2 products + DPP row reductions, up to 4 heads per wave */
+#define PKV_PATH_MFMA 2        /* gfx950 16x16x32 / 16x16x16 MFMA for QK^T and PV, 16 heads per wave */
 
 /* Work schedules (pkv_decode_schedule). */
 #define PKV_SCHED_SINGLE 1     /* one pass per (b, kv head, head group); out written directly */
@@ -66,7 +66,7 @@ typedef struct pkv_decode_desc {
     int32_t dtype;              /* PKV_DTYPE_F16 or PKV_DTYPE_BF16 (q, caches and out share it) */
     int32_t path;               /* PKV_PATH_* */
     int32_t split_tokens;       /* num_splits == 0 only: tokens per split window (multiple of 16);
-                                   0 = chosen by the library */
+                                   0 = the tile-balanced schedule */
     int32_t reserved;           /* must be 0 */
     void* workspace;            /* device memory for split partials; may be NULL when splits == 1 */
     size_t workspace_bytes;
@@ -84,13 +84,13 @@ typedef struct pkv_decode_desc {
  * north-star argument order and an explicit stream.
  *
  * num_splits follows flash-attn (scripts/evaluate_flashattn_submission.py:246):
- *   0 = heuristic: on the MFMA path with desc->split_tokens == 0, the
- *       tile-balanced schedule — all rows' 16-token tiles (times KV heads and
- *       head groups) are laid end to end and dealt in equal shares to one
- *       workgroup of waves per CU, which read cache_seqlens on the device, so
- *       every wave streams the same bytes however ragged the rows are, and a
- *       combine merges the rows that more than one wave touched.  Otherwise
- *       fixed windows of split_tokens tokens (chosen from the shape when 0);
+ *   0 = heuristic: with desc->split_tokens == 0, the tile-balanced schedule —
+ *       all rows' 16-token tiles (times KV heads and head groups) are laid end
+ *       to end and dealt in equal shares to one workgroup of waves per CU,
+ *       which read cache_seqlens on the device, so every wave streams the same
+ *       bytes however ragged the rows are, and a combine merges the rows that
+ *       more than one wave touched.  With desc->split_tokens > 0, fixed
+ *       windows of that many tokens;
  *   1 = single pass writing `out` directly;
  *   n > 1 = forced: each row's valid pages are divided into n near-equal
  *       ranges as the reference does (clamped to [1, min(PKV_MAX_SPLITS,

@@ -113,18 +113,9 @@ def test_split_resolution():
     assert pagedkv.num_splits_for(d2, 10_000) == pagedkv.PKV_MAX_SPLITS
     assert pagedkv.schedule_for(d, 1) == pagedkv.PKV_SCHED_SINGLE
     assert pagedkv.schedule_for(d, 7) == pagedkv.PKV_SCHED_PAGES
-    # window heuristic (VALU path, or an explicit window)
-    v = base_desc(path=pagedkv.PKV_PATH_VALU)
-    assert pagedkv.schedule_for(v, 0) == pagedkv.PKV_SCHED_WINDOWS
-    auto = pagedkv.num_splits_for(v, 0)
-    assert 1 <= auto <= 64
-    # short rows never split below the minimum split length
-    assert pagedkv.num_splits_for(base_desc(max_seqlen=200, path=pagedkv.PKV_PATH_VALU), 0) == 1
-    assert pagedkv.schedule_for(base_desc(max_seqlen=200, path=pagedkv.PKV_PATH_VALU), 0) == pagedkv.PKV_SCHED_SINGLE
-    # tiny batch with a long context gets many splits, capped by PKV_MAX_SPLITS
-    many = pagedkv.num_splits_for(base_desc(batch=1, num_heads=8, num_heads_k=1, max_seqlen=131072,
-                                            block_table_stride=2048, path=pagedkv.PKV_PATH_VALU), 0)
-    assert 64 <= many <= pagedkv.PKV_MAX_SPLITS
+    # the heuristic is the tile-balanced schedule on both kernel families
+    for path in (pagedkv.PKV_PATH_VALU, pagedkv.PKV_PATH_MFMA):
+        assert pagedkv.schedule_for(base_desc(path=path), 0) == pagedkv.PKV_SCHED_TILES
 
 
 TILE_WAVES = 4      # waves per workgroup of the tile-balanced kernel
@@ -152,6 +143,12 @@ def test_tile_schedule_plan():
     # an explicit window or forced splits leave the tile schedule
     assert pagedkv.schedule_for(base_desc(split_tokens=512), 0) == pagedkv.PKV_SCHED_WINDOWS
     assert pagedkv.schedule_for(d, 4) == pagedkv.PKV_SCHED_PAGES
+    # VALU math: at most 4 heads per partial slot, head groups of 4
+    v = base_desc(num_heads=64, num_heads_k=8, path=pagedkv.PKV_PATH_VALU)   # group 8
+    workers = pagedkv.num_splits_for(v, 0)
+    streams = 32 * 8 * 2
+    rows = (workers + streams) * 4
+    assert pagedkv.workspace_size(v, 0) == align(rows * 128 * 4) + align(rows * 4)
 
 
 def test_auto_path_is_a_kernel_family():
@@ -171,14 +168,10 @@ def test_run_kernel_rejects_unsupported_modes_without_launching():
 
 
 def test_split_token_windows():
-    d = base_desc(path=pagedkv.PKV_PATH_VALU)
-    # heuristic: fixed windows, a power of two of at least 256 tokens
-    tok = pagedkv.split_tokens_for(d, 0)
-    assert tok >= 256 and tok & (tok - 1) == 0
-    assert pagedkv.num_splits_for(d, 0) == -(-4096 // tok)
     # an explicit window is honoured (on either path)
     for path in (pagedkv.PKV_PATH_VALU, pagedkv.PKV_PATH_MFMA):
         d = base_desc(split_tokens=512, path=path)
+        assert pagedkv.schedule_for(d, 0) == pagedkv.PKV_SCHED_WINDOWS
         assert pagedkv.split_tokens_for(d, 0) == 512
         assert pagedkv.num_splits_for(d, 0) == 8
     # forced split counts are page-balanced (no window)
