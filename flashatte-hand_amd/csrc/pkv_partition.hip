@@ -304,6 +304,44 @@ struct MfmaMath {
             p.part_lse[pi] = a.l > 0.f ? a.m + fast_log2(a.l) : kNegInf;
         }
     }
+
+    // Online-softmax merge of another wave's finished accumulator (same lane layout).
+    __device__ static void merge(Acc& a, const Acc& b) {
+        const float m = fmaxf(a.m, b.m);
+        const float sa = a.m == kNegInf ? 0.f : fast_exp2(a.m - m);
+        const float sb = b.m == kNegInf ? 0.f : fast_exp2(b.m - m);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            a.o[dt] = a.o[dt] * sa + b.o[dt] * sb;
+        }
+        a.l = a.l * sa + b.l * sb;
+        a.m = m;
+    }
+
+    // Accumulator through LDS, one float per lane and field (conflict-free).
+    static constexpr int kAccFloats = 4 * DT + 2;
+    __device__ static void store_lds(const Acc& a, float* base, int lane) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                base[(4 * dt + i) * 64 + lane] = a.o[dt][i];
+            }
+        }
+        base[4 * DT * 64 + lane] = a.m;
+        base[(4 * DT + 1) * 64 + lane] = a.l;
+    }
+    __device__ static void load_lds(Acc& a, const float* base, int lane) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a.o[dt][i] = base[(4 * dt + i) * 64 + lane];
+            }
+        }
+        a.m = base[4 * DT * 64 + lane];
+        a.l = base[(4 * DT + 1) * 64 + lane];
+    }
 };
 
 // ---------------------------------------------------------------- VALU math
@@ -469,6 +507,47 @@ struct ValuMath {
             }
         }
     }
+
+    // Online-softmax merge of another wave's finished accumulator (same lane layout).
+    __device__ static void merge(Acc& a, const Acc& b) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+            const float m = fmaxf(a.m[h], b.m[h]);
+            const float sa = a.m[h] == kNegInf ? 0.f : fast_exp2(a.m[h] - m);
+            const float sb = b.m[h] == kNegInf ? 0.f : fast_exp2(b.m[h] - m);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                a.o[h][e] = a.o[h][e] * sa + b.o[h][e] * sb;
+            }
+            a.l[h] = a.l[h] * sa + b.l[h] * sb;
+            a.m[h] = m;
+        }
+    }
+
+    // Accumulator through LDS, one float per lane and field (conflict-free).
+    static constexpr int kAccFloats = NH * (E + 2);
+    __device__ static void store_lds(const Acc& a, float* base, int lane) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                base[(h * E + e) * 64 + lane] = a.o[h][e];
+            }
+            base[(NH * E + h) * 64 + lane] = a.m[h];
+            base[(NH * E + NH + h) * 64 + lane] = a.l[h];
+        }
+    }
+    __device__ static void load_lds(Acc& a, const float* base, int lane) {
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                a.o[h][e] = base[(h * E + e) * 64 + lane];
+            }
+            a.m[h] = base[(NH * E + h) * 64 + lane];
+            a.l[h] = base[(NH * E + NH + h) * 64 + lane];
+        }
+    }
 };
 
 // ---------------------------------------------------------------- tile pipeline
@@ -628,6 +707,76 @@ void partition_split_kernel(PartitionParams p) {
     }
 }
 
+// Split schedules with fewer items than CUs (small batches): one workgroup per
+// item, its waves taking consecutive quarters of the item's tiles; each wave
+// then parks its finished accumulator in its own LDS tile and wave 0 merges
+// the four (online-softmax merge) and writes the item's output or partial.
+// Still one pass per item and no workspace: only the latency changes.
+template <typename Math, int D, bool WIDE, int DEPTH>
+__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
+void partition_item_group_kernel(PartitionParams p) {
+    constexpr int kWaves = kWavesPerGroup;
+    static_assert(Math::kAccFloats * 64 * sizeof(float) <= 2 * VTile<D>::kElems * sizeof(uint16_t),
+                  "accumulator must fit the wave's LDS tiles");
+    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][2 * VTile<D>::kElems];
+
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const Item it = decode_item(static_cast<int32_t>(blockIdx.x), p);
+    const int g_first = it.hg * Math::kHeads;
+    const int heads_here = min(Math::kHeads, p.group - g_first);
+    const int64_t bh_first = static_cast<int64_t>(it.b) * p.num_heads + it.kvh * p.group + g_first;
+    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(it.b) * p.bt_stride;
+
+    typename Math::Q q;
+    Math::load_q(p, bh_first, heads_here, lane, q);
+    const int seqlen = min(p.seqlens[it.b], p.row_cap);
+    const TokenRange range = split_tokens_of(seqlen, p.page_shift, it.split, p.splits, p.split_tokens);
+    if (range.begin >= range.end) {
+        // As in partition_split_kernel: zeros for an empty row, nothing for an empty split.
+        if (p.splits == 1 && wave == 0) {
+            constexpr int CH = D / 8;
+            for (int idx = lane; idx < heads_here * CH; idx += 64) {
+                const int g = idx / CH;
+                const int c = idx % CH;
+                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + c * 8) = make_uint4(0u, 0u, 0u, 0u);
+            }
+        }
+        return;
+    }
+    const int ntiles = (range.end - range.begin + 15) >> 4;
+    const int per = (ntiles + kWaves - 1) / kWaves;
+    const int sub_begin = range.begin + 16 * min(ntiles, wave * per);
+    const int sub_end = min(range.end, range.begin + 16 * min(ntiles, (wave + 1) * per));
+
+    typename Math::Acc acc;
+    if (sub_begin < sub_end) {
+        const int win_base = sub_begin >> p.page_shift;
+        const int win = load_page_window(bt_row, win_base, (sub_end - 1) >> p.page_shift, lane, p.num_pages);
+        attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], sub_begin, sub_end, lane,
+                                           it.kvh, acc);
+    } else {
+        Math::init(acc);
+        Math::finish(acc);
+    }
+    Math::store_lds(acc, reinterpret_cast<float*>(lds_tiles[wave]), lane);
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) {
+        typename Math::Acc other;
+        Math::load_lds(other, reinterpret_cast<const float*>(lds_tiles[k]), lane);
+        Math::merge(acc, other);
+    }
+    if (p.splits == 1) {
+        Math::write_final(p, bh_first, heads_here, acc, lane);
+    } else {
+        Math::write_partial(p, bh_first * p.splits + it.split, p.splits, heads_here, acc, lane);
+    }
+}
+
 // Tile-balanced schedule (streams, units, shares and slots as defined with
 // row_tiles and make_tile_plan in pkv_device.h): wave w streams its share,
 // segment by segment.  A segment that is a whole stream is written to the
@@ -712,8 +861,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
 }
 
 // Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
-// whole chip busy and streams fastest with one; the split schedules take two
-// when their few waves (fewer than one per CU) are latency-bound.
+// whole chip busy and streams fastest with one; split schedules with fewer
+// items than CUs are latency-bound and take two.
 #ifndef PKV_MFMA_DEPTH
 #define PKV_MFMA_DEPTH 1
 #endif
@@ -734,12 +883,14 @@ static void launch_tiles(const PartitionParams& p, hipStream_t stream, const Lau
 
 template <typename Math, int D, bool WIDE>
 static void launch_split(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    const dim3 grid(p.num_groups);
     const dim3 block(64 * kWavesPerGroup);
     if (p.num_items < kComputeUnits) {
-        launch_kernel(partition_split_kernel<Math, D, WIDE, kSplitDepthFewItems>, grid, block, 0, stream, ev, p);
+        // Fewer items than CUs: a workgroup per item, latency-bound, two tiles in flight.
+        launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems>, dim3(p.num_items), block, 0,
+                      stream, ev, p);
     } else {
-        launch_kernel(partition_split_kernel<Math, D, WIDE, PKV_MFMA_DEPTH>, grid, block, 0, stream, ev, p);
+        launch_kernel(partition_split_kernel<Math, D, WIDE, PKV_MFMA_DEPTH>, dim3(p.num_groups), block, 0, stream,
+                      ev, p);
     }
 }
 
