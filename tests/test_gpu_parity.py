@@ -227,6 +227,18 @@ def test_tiles_more_workers_than_tiles(rng):
     assert (got[2] == 0).all()
 
 
+def test_tiles_wide_block_table_rows(rng):
+    """Rows addressable up to 2^24+ tokens (block_table_stride * P): the device-side
+    row scan leaves its 32-bit fast path; short rows must still come out right."""
+    q, k, v, bt, sl = make_case(rng, B=3, H=8, Hk=2, D=64, P=1024, seqlens=[3000, 10, 1030], dtype=1,
+                                stride=20000)
+    assert bt.shape[1] * 1024 > (1 << 24)
+    announce("tiles-wide-rows", bt.shape)
+    got = po.bits_to_f32(run_hip(q, k, v, bt, sl, 0.125, 1, 0, 2, max_seqlen=3000), 1)
+    want = po.decode_f64(q, k, v, bt, sl, 0.125, 1)
+    assert np.max(np.abs(got - want)) < TOL[1]
+
+
 def test_tiles_all_rows_empty(rng):
     q, k, v, bt, sl = make_case(rng, B=4, H=8, Hk=2, D=128, P=16, seqlens=[0, 0, 0, 0], dtype=1)
     announce("tiles-empty")
