@@ -10,6 +10,12 @@ MALL).  Prints ONE JSON line on stdout.
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--sets 3]
                     [--path 0|1|2] [--splits N] [--all] [--json-out FILE]
+
+`--op append` instead times the paged KV-cache append (slot-mapped copy of
+every token of the config's rows, i.e. the prefill write of that batch);
+`--op decode_append` times the decode step with one new token per row
+appended inside the call (flash_attn_with_kvcache(k=, v=)), the attended rows
+having the config's lengths.
 """
 from __future__ import annotations
 
@@ -186,6 +192,134 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     return res
 
 
+def run_append(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
+    """Slot-mapped append of every token of the config's rows into a scattered pool."""
+    from pagedkv.configs import make_config, torch_dtype
+
+    cfg = make_config(name)
+    T = int(cfg.seqlens.clip(min=0).sum())
+    Hk, D, P = cfg.num_heads_k, cfg.head_dim, cfg.page_size
+    pool = (T + P - 1) // P + 64
+    dt = torch_dtype(cfg)
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(cfg.seed)
+    n_sets = max(1, args.sets)
+    caches = [(torch.empty((pool, P, Hk, D), dtype=dt, device=dev), torch.empty((pool, P, Hk, D), dtype=dt, device=dev))
+              for _ in range(n_sets)]
+    news = [(torch.randn((T, Hk, D), dtype=dt, device=dev, generator=g),
+             torch.randn((T, Hk, D), dtype=dt, device=dev, generator=g)) for _ in range(n_sets)]
+    slots = [torch.randperm(pool * P, device=dev, generator=g)[:T] for _ in range(n_sets)]
+    desc = pagedkv.make_desc(batch=0, num_heads=0, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=pool,
+                             block_table_stride=0, dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16"
+                             else pagedkv.PKV_DTYPE_BF16)
+    lib = pagedkv._lib.load()
+    sh = torch.cuda.current_stream(dev).cuda_stream
+
+    def call(i):
+        (kc, vc), (kn, vn), sm = caches[i % n_sets], news[i % n_sets], slots[i % n_sets]
+        st = lib.pkv_reshape_and_cache(kn.data_ptr(), vn.data_ptr(), kc.data_ptr(), vc.data_ptr(), sm.data_ptr(), T,
+                                       ctypes.byref(desc), sh)
+        if st != 0:
+            raise pagedkv.PkvError(st, "pkv_reshape_and_cache")
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    t_start, t_end = events.create(2)
+    events.hip.hipEventRecord(t_start, sh)
+    for i in range(args.steps):
+        call(i)
+    events.hip.hipEventRecord(t_end, sh)
+    torch.cuda.synchronize()
+    ms = events.elapsed_ms(t_start, t_end) / args.steps
+    events.destroy([t_start, t_end])
+    row = Hk * D * 2
+    # Algorithmic bytes: K and V rows read once and written once, plus the 8-byte slot per token.
+    alg = T * (4 * row + 8)
+    gbps = alg / (ms * 1e-3) / 1e9
+    return {"cfg": cfg, "tokens": T, "ms": ms, "gbps": gbps, "alg": alg, "pool_pages": pool,
+            "host": (news[0], slots[0], pool)}
+
+
+def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
+    """Decode step with one new token per row appended in the call; rows end at the config's lengths."""
+    from pagedkv.configs import make_config, make_tensors
+
+    cfg = make_config(name)
+    sets = [make_tensors(cfg, "cuda", seed=cfg.seed + 7919 * i) for i in range(max(1, args.sets))]
+    dev = torch.device("cuda")
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    base = sets[0]
+    desc = pagedkv.make_desc(
+        batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k, head_dim=cfg.head_dim,
+        page_size=cfg.page_size, num_pages=base["k_cache"].shape[0], block_table_stride=cfg.block_table.shape[1],
+        dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
+        max_seqlen=int(cfg.seqlens.max()) - 1, path=args.path,
+    )
+    splits_req = args.splits if args.splits is not None else cfg.num_splits
+    lib = pagedkv._lib.load()
+    ws_bytes = lib.pkv_decode_append_workspace_size(ctypes.byref(desc), splits_req, 1)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+    desc.workspace = ws.data_ptr()
+    desc.workspace_bytes = ws_bytes
+    prev = [(s["cache_seqlens"] - 1).clamp(min=0).to(torch.int32).contiguous() for s in sets]
+    shape = (cfg.batch, 1, cfg.num_heads_k, cfg.head_dim)
+    news = [(torch.randn(shape, device=dev).to(base["k_cache"].dtype),
+             torch.randn(shape, device=dev).to(base["k_cache"].dtype)) for _ in sets]
+    outs = [torch.empty_like(s["q"]) for s in sets]
+
+    def call(i):
+        s, (kn, vn), sl, o = sets[i % len(sets)], news[i % len(sets)], prev[i % len(sets)], outs[i % len(sets)]
+        st = lib.pkv_decode_append(s["q"].data_ptr(), kn.data_ptr(), vn.data_ptr(), s["k_cache"].data_ptr(),
+                                   s["v_cache"].data_ptr(), s["block_table"].data_ptr(), sl.data_ptr(), 1,
+                                   float(cfg.scale), splits_req, o.data_ptr(), ctypes.byref(desc), sh)
+        if st != 0:
+            raise pagedkv.PkvError(st, "pkv_decode_append")
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    t_start, t_end = events.create(2)
+    events.hip.hipEventRecord(t_start, sh)
+    for i in range(args.steps):
+        call(i)
+    events.hip.hipEventRecord(t_end, sh)
+    torch.cuda.synchronize()
+    ms = events.elapsed_ms(t_start, t_end) / args.steps
+    events.destroy([t_start, t_end])
+    return {"cfg": cfg, "ms": ms, "kv_gbps": cfg.kv_bytes() / (ms * 1e-3) / 1e9}
+
+
+def cpu_append_baseline(res: dict, torch, budget_s: float) -> dict:
+    """The numpy restatement of the slot-mapped append on the host, over a bounded slice of the tokens."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import numpy as np
+
+    import pkv_oracle as po
+
+    (kn, vn), slots, pool = res["host"]
+    n = min(res["tokens"], 16384)
+    k = kn[:n].view(torch.int16).cpu().numpy().view(np.uint16)
+    v = vn[:n].view(torch.int16).cpu().numpy().view(np.uint16)
+    cfg = res["cfg"]
+    # A host pool with room for the slice, written in place, slots scattered over it.
+    pages = (n + cfg.page_size - 1) // cfg.page_size + 64
+    sm = np.random.default_rng(cfg.seed).permutation(pages * cfg.page_size)[:n].astype(np.int64)
+    kc = np.zeros((pages, cfg.page_size, cfg.num_heads_k, cfg.head_dim), dtype=np.uint16)
+    vc = np.zeros_like(kc)
+    times = []
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and len(times) < 200:
+        a = time.perf_counter()
+        po.reshape_and_cache(kc, vc, k, v, sm, inplace=True)
+        times.append(time.perf_counter() - a)
+    t = sorted(times)[len(times) // 2]
+    row = cfg.num_heads_k * cfg.head_dim * 2
+    return {"value": round(n * (4 * row + 8) / t / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} in-place numpy appends of {n} of the {res['tokens']} tokens "
+                      f"(median {t * 1e3:.1f} ms)"}
+
+
 def cpu_baseline(res: dict, torch, budget_s: float) -> dict:
     """The oracle's fp32 restatement of the reference's scalar decode on the host cores."""
     sys.path.insert(0, str(REPO / "oracle"))
@@ -233,6 +367,9 @@ def main() -> int:
     ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--op", choices=("decode", "append", "decode_append"), default="decode",
+                    help="decode (default, the headline); append: paged KV-cache append; decode_append: "
+                         "decode with one new token per row appended in the call")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of benchmarking, run a plain device copy of MIB MiB (read + write) five times; "
                          "used to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -260,6 +397,8 @@ def main() -> int:
         print(json.dumps({"calibrate_copy_bytes_read": n * 4, "calibrate_copy_bytes_written": n * 4}), flush=True)
         return 0
     events = HipEvents()
+    if args.op != "decode":
+        return run_op(args, torch, pagedkv, events)
     names = [args.config] + ([n for n in ("c1", "c2", "c3", "c4", "c5") if n != args.config] if args.all else [])
     lines = []
     headline = None
@@ -309,6 +448,40 @@ def main() -> int:
             for ln in lines:
                 f.write(json.dumps(ln) + "\n")
     print(json.dumps(headline), flush=True)
+    return 0
+
+
+def run_op(args, torch, pagedkv, events: HipEvents) -> int:
+    common = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded N(0,1) rows, random slots)"}
+    if args.op == "append":
+        res = run_append(args.config, args, torch, pagedkv, events)
+        cfg = res["cfg"]
+        line = {"metric": "paged KV-cache append HBM GB/s (slot-mapped prefill write of the config's rows)",
+                "value": round(res["gbps"], 1), "unit": "GB/s", **common, "ms_per_step": round(res["ms"], 5),
+                "dtype": cfg.dtype,
+                "config": {"workload": f"append of {res['tokens']} tokens ({cfg.name} geometry)",
+                           "num_heads_k": cfg.num_heads_k, "head_dim": cfg.head_dim, "page_size": cfg.page_size,
+                           "pool_pages": res["pool_pages"], "kv_sets": args.sets},
+                "roofline": {"bound": "hbm", "achieved": round(res["gbps"], 1), "peak": HBM_PEAK_GBPS,
+                             "unit": "GB/s", "frac": round(res["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                             "kernel": "append", "alg_bytes_per_launch": int(res["alg"])},
+                "cpu_baseline": None if args.no_cpu else cpu_append_baseline(res, torch, args.cpu_budget)}
+        print(f"[bench] append {res['tokens']} tokens: {res['ms'] * 1e3:.2f} us, {res['gbps']:.1f} GB/s "
+              f"({100 * res['gbps'] / HBM_PEAK_GBPS:.1f}% of peak)", file=sys.stderr, flush=True)
+    else:
+        res = run_decode_append(args.config, args, torch, pagedkv, events)
+        cfg = res["cfg"]
+        line = {"metric": "KV-stream HBM GB/s of a decode step with a one-token append per row",
+                "value": round(res["kv_gbps"], 1), "unit": "GB/s", **common, "ms_per_step": round(res["ms"], 5),
+                "dtype": cfg.dtype, "config": {**cfg.describe(), "workload": "decode_append", "seqlen_new": 1},
+                "us_per_call": round(res["ms"] * 1e3, 2), "cpu_baseline": None}
+        print(f"[bench] decode_append {cfg.name}: {res['ms'] * 1e3:.2f} us/call, {res['kv_gbps']:.1f} GB/s KV",
+              file=sys.stderr, flush=True)
+    if args.json_out:
+        with open(args.json_out, "a") as f:
+            f.write(json.dumps(line) + "\n")
+    print(json.dumps(line), flush=True)
     return 0
 
 

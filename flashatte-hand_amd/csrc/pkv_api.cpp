@@ -199,64 +199,12 @@ std::mutex g_legacy_mutex;
 void* g_legacy_ws = nullptr;
 size_t g_legacy_ws_bytes = 0;
 
-} // namespace
-
-extern "C" {
-
-const char* pkv_strerror(int status) {
-    switch (status) {
-    case PKV_OK: return "ok";
-    case PKV_EINVAL: return "invalid argument";
-    case PKV_EUNSUPPORTED: return "unsupported shape or dtype";
-    case PKV_ENOWORKSPACE: return "workspace missing or too small";
-    case PKV_ELAUNCH: return "HIP launch failed";
-    default: return "unknown status";
-    }
-}
-
-int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits) {
-    Resolved r;
-    if (resolve(desc, r) != PKV_OK) {
-        return 0;
-    }
-    return resolve_splits(desc, r, num_splits).splits;
-}
-
-int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
-    Resolved r;
-    if (resolve(desc, r) != PKV_OK) {
-        return 0;
-    }
-    return resolve_splits(desc, r, num_splits).split_tokens;
-}
-
-int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits) {
-    Resolved r;
-    if (resolve(desc, r) != PKV_OK) {
-        return 0;
-    }
-    return resolve_splits(desc, r, num_splits).schedule;
-}
-
-int pkv_decode_path(const pkv_decode_desc* desc) {
-    Resolved r;
-    if (resolve(desc, r) != PKV_OK) {
-        return 0;
-    }
-    return r.path;
-}
-
-size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
-    Resolved r;
-    if (resolve(desc, r) != PKV_OK) {
-        return 0;
-    }
-    return workspace_bytes(r, resolve_splits(desc, r, num_splits));
-}
-
-int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
-               const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
-               const pkv_decode_desc* desc, void* stream) {
+// pkv_decode: validation, then (when `launch`) the partition and combine
+// launches.  With launch == false only the checks run, so a caller that
+// enqueues other work first can fail before touching anything.
+int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
+                const pkv_decode_desc* desc, void* stream, bool launch) {
     Resolved r;
     int st = resolve(desc, r);
     if (st != PKV_OK) {
@@ -282,6 +230,9 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
     const int64_t items = tiles ? 0 : r.B * r.Hk * r.head_groups * splits;
     if (items > INT32_MAX || (tiles && static_cast<int64_t>(plan.splits) + r.B * streams_per_row(r) > INT32_MAX)) {
         return PKV_EUNSUPPORTED;
+    }
+    if (!launch) {
+        return PKV_OK;
     }
 
     pkv::PartitionParams p{};
@@ -358,6 +309,217 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
         }
     }
     return PKV_OK;
+}
+
+// Append launch parameters shared by both index forms.
+pkv::AppendParams append_params(const Resolved& r, const pkv_decode_desc* d, const void* k_new, const void* v_new,
+                                void* k_cache, void* v_cache, int64_t tokens) {
+    pkv::AppendParams a{};
+    a.k_new = static_cast<const uint4*>(k_new);
+    a.v_new = static_cast<const uint4*>(v_new);
+    a.k_cache = static_cast<uint4*>(k_cache);
+    a.v_cache = static_cast<uint4*>(v_cache);
+    a.tokens = tokens;
+    a.num_slots = d->num_pages * r.P;
+    a.row_cap = d->block_table_stride * r.P;
+    a.chunks = static_cast<int32_t>(r.Hk * r.D / 8);
+    a.page_shift = r.page_shift;
+    a.bt_stride = static_cast<int32_t>(d->block_table_stride);
+    a.num_pages = static_cast<int32_t>(d->num_pages);
+    a.batch = static_cast<int32_t>(r.B);
+    return a;
+}
+
+bool append_pointers_ok(const void* k_new, const void* v_new, const void* k_cache, const void* v_cache) {
+    return k_new != nullptr && v_new != nullptr && k_cache != nullptr && v_cache != nullptr && aligned16(k_new) &&
+           aligned16(v_new) && aligned16(k_cache) && aligned16(v_cache);
+}
+
+// Rows of new tokens the kernel indexes with 32-bit row and in-row counts.
+bool append_fits(const Resolved& r, int64_t seqlen_new) {
+    return seqlen_new <= INT32_MAX && r.B * seqlen_new <= (int64_t{1} << 40) && r.Hk * r.D / 8 <= INT32_MAX;
+}
+
+// Workspace of pkv_decode_append: the per-row lengths after the append, then
+// the attention's own workspace for the longer rows.
+pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
+    pkv_decode_desc a = *d;
+    a.max_seqlen = d->max_seqlen > 0 ? d->max_seqlen + seqlen_new : 0;
+    return a;
+}
+
+} // namespace
+
+extern "C" {
+
+const char* pkv_strerror(int status) {
+    switch (status) {
+    case PKV_OK: return "ok";
+    case PKV_EINVAL: return "invalid argument";
+    case PKV_EUNSUPPORTED: return "unsupported shape or dtype";
+    case PKV_ENOWORKSPACE: return "workspace missing or too small";
+    case PKV_ELAUNCH: return "HIP launch failed";
+    default: return "unknown status";
+    }
+}
+
+int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits).splits;
+}
+
+int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits).split_tokens;
+}
+
+int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return resolve_splits(desc, r, num_splits).schedule;
+}
+
+int pkv_decode_path(const pkv_decode_desc* desc) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return r.path;
+}
+
+size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    return workspace_bytes(r, resolve_splits(desc, r, num_splits));
+}
+
+int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+               const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
+               const pkv_decode_desc* desc, void* stream) {
+    return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, desc, stream,
+                       true);
+}
+
+int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache, const int32_t* block_table,
+                  const int32_t* cache_seqlens, int64_t seqlen_new, const pkv_decode_desc* desc, void* stream) {
+    Resolved r;
+    const int st = resolve(desc, r);
+    if (st != PKV_OK) {
+        return st;
+    }
+    if (seqlen_new < 0 || block_table == nullptr || cache_seqlens == nullptr ||
+        !append_pointers_ok(k_new, v_new, k_cache, v_cache)) {
+        return PKV_EINVAL;
+    }
+    if (!append_fits(r, seqlen_new)) {
+        return PKV_EUNSUPPORTED;
+    }
+    pkv::AppendParams a = append_params(r, desc, k_new, v_new, k_cache, v_cache, r.B * seqlen_new);
+    a.block_table = block_table;
+    a.seqlens = cache_seqlens;
+    a.n_new = static_cast<int32_t>(seqlen_new);
+    return pkv::launch_append(a, static_cast<hipStream_t>(stream), {}) == hipSuccess ? PKV_OK : PKV_ELAUNCH;
+}
+
+int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, const pkv_decode_desc* desc,
+                          void* stream) {
+    if (desc == nullptr) {
+        return PKV_EINVAL;
+    }
+    // Only the cache geometry matters here: the row-shaped fields get
+    // placeholders so the shared validation applies to the rest.
+    pkv_decode_desc g = *desc;
+    g.batch = 1;
+    g.num_heads = g.num_heads_k;
+    g.block_table_stride = 1;
+    g.max_seqlen = 0;
+    g.split_tokens = 0;
+    Resolved r;
+    const int st = resolve(&g, r);
+    if (st != PKV_OK) {
+        return st;
+    }
+    if (num_tokens < 0 || slot_mapping == nullptr || !append_pointers_ok(key, value, k_cache, v_cache)) {
+        return PKV_EINVAL;
+    }
+    if (num_tokens > (int64_t{1} << 40)) {
+        return PKV_EUNSUPPORTED;
+    }
+    pkv::AppendParams a = append_params(r, &g, key, value, k_cache, v_cache, num_tokens);
+    a.slot_mapping = slot_mapping;
+    a.n_new = 1;
+    return pkv::launch_append(a, static_cast<hipStream_t>(stream), {}) == hipSuccess ? PKV_OK : PKV_ELAUNCH;
+}
+
+size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new) {
+    Resolved r;
+    if (seqlen_new < 0 || resolve(desc, r) != PKV_OK) {
+        return 0;
+    }
+    if (seqlen_new == 0) {
+        return pkv_decode_workspace_size(desc, num_splits);
+    }
+    const pkv_decode_desc a = appended_desc(desc, seqlen_new);
+    return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + pkv_decode_workspace_size(&a, num_splits);
+}
+
+int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_new,
+                      float softmax_scale, int num_splits, void* out, const pkv_decode_desc* desc, void* stream) {
+    if (seqlen_new == 0) {
+        return pkv_decode(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, desc,
+                          stream);
+    }
+    Resolved r;
+    int st = resolve(desc, r);
+    if (st != PKV_OK) {
+        return st;
+    }
+    if (seqlen_new < 0 || block_table == nullptr || cache_seqlens == nullptr ||
+        !append_pointers_ok(k_new, v_new, k_cache, v_cache)) {
+        return PKV_EINVAL;
+    }
+    if (!append_fits(r, seqlen_new)) {
+        return PKV_EUNSUPPORTED;
+    }
+    // The per-row lengths lead the workspace; the attention's partials follow.
+    const size_t lens_bytes = align_up(static_cast<size_t>(r.B) * sizeof(int32_t));
+    if (desc->workspace == nullptr || desc->workspace_bytes < lens_bytes || !aligned16(desc->workspace)) {
+        return PKV_ENOWORKSPACE;
+    }
+    int32_t* lens = static_cast<int32_t*>(desc->workspace);
+    pkv_decode_desc a = appended_desc(desc, seqlen_new);
+    a.workspace = static_cast<char*>(desc->workspace) + lens_bytes;
+    a.workspace_bytes = desc->workspace_bytes - lens_bytes;
+    if (pkv_decode_workspace_size(&a, num_splits) == 0) {
+        a.workspace = nullptr;
+        a.workspace_bytes = 0;
+    }
+    // Every check of the attention runs before the cache is written.
+    st = decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, false);
+    if (st != PKV_OK) {
+        return st;
+    }
+    pkv::AppendParams ap = append_params(r, desc, k_new, v_new, k_cache, v_cache, r.B * seqlen_new);
+    ap.block_table = block_table;
+    ap.seqlens = cache_seqlens;
+    ap.seqlens_out = lens;
+    ap.n_new = static_cast<int32_t>(seqlen_new);
+    if (pkv::launch_append(ap, static_cast<hipStream_t>(stream), {}) != hipSuccess) {
+        return PKV_ELAUNCH;
+    }
+    return decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, true);
 }
 
 void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_paged, void* output,

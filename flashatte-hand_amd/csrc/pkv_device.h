@@ -63,6 +63,29 @@ struct CombineParams {
     int32_t heads_per_wave; // query heads per stream (16 MFMA, 1/2/4 VALU)
 };
 
+// Paged KV-cache append (pkv_append.hip): one 16-byte chunk of K and of V per
+// thread.  A token row is Hk * D 16-bit elements, contiguous in the new-token
+// tensors ([tokens, Hk, D]) and in its cache slot ([num_pages, P, Hk, D]).
+struct AppendParams {
+    const uint4* k_new;           // [tokens, Hk, D]: token i = b * n_new + j, or i of the slot mapping
+    const uint4* v_new;
+    uint4* k_cache;               // [num_pages, P, Hk, D]
+    uint4* v_cache;
+    const int32_t* block_table;   // block-table form: [B, bt_stride]
+    const int32_t* seqlens;       // block-table form: position of token j of row b = max(seqlens[b], 0) + j
+    const int64_t* slot_mapping;  // slot form: flat slot page * P + slot of token i; < 0 = padding
+    int32_t* seqlens_out;         // optional (block-table form): max(seqlens[b], 0) + n_new per row
+    int64_t tokens;               // token rows to write
+    int64_t num_slots;            // num_pages * P
+    int64_t row_cap;              // positions a block-table row addresses (bt_stride * P)
+    int32_t chunks;               // 16-byte chunks per token row (Hk * D / 8)
+    int32_t n_new;                // block-table form: new tokens per row
+    int32_t page_shift;           // log2(P)
+    int32_t bt_stride;
+    int32_t num_pages;
+    int32_t batch;
+};
+
 constexpr float kNegInf = -__builtin_huge_valf();
 
 // ---------------------------------------------------------------- 16-bit <-> fp32

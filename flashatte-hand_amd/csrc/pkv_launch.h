@@ -39,4 +39,8 @@ hipError_t launch_partition(const PartitionParams& p, bool mfma, bool bf16, int 
 hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,
                           const LaunchEvents& ev);
 
+// Paged KV-cache append: slot-mapping form when p.slot_mapping is set, else
+// the block-table form.
+hipError_t launch_append(const AppendParams& p, hipStream_t stream, const LaunchEvents& ev);
+
 } // namespace pkv

@@ -9,6 +9,10 @@ Two call surfaces over the C ABI of ``libpkv_decode.so``:
 * :func:`run_kernel` — the reference's 15-argument torch binding
   (scripts/evaluate_flashattn_submission.py:46-78 -> best_flashattn_kvcache_decode.cu:1186).
 
+and the paged KV-cache append that precedes a decode step: ``k`` / ``v`` of
+:func:`flash_attn_with_kvcache` (flash-attn 2.6.3 semantics), :func:`append_kv`
+(block-table positions) and :func:`reshape_and_cache_flash` (flat slots).
+
 Both run the gfx950 HIP kernels; there is no CPU or PyTorch fallback.  Torch
 is used only to hand over device pointers and the current HIP stream.
 """
@@ -42,6 +46,8 @@ from ._lib import (  # noqa: F401  (re-exported constants)
 __all__ = [
     "make_desc",
     "decode",
+    "append_kv",
+    "reshape_and_cache_flash",
     "flash_attn_with_kvcache",
     "run_kernel",
     "workspace_size",
@@ -147,11 +153,17 @@ def decode(
     workspace=None,
     stream=None,
     prof_events: int = 0,
+    k_new=None,
+    v_new=None,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,1,H,D]).
 
+    With ``k_new`` / ``v_new`` ([B, seqlen_new, Hk, D]) the new tokens are first
+    written into the caches at each row's ``cache_seqlens`` position and the
+    attention covers ``cache_seqlens + seqlen_new`` tokens (flash-attn's
+    ``flash_attn_with_kvcache(k=, v=)``); ``cache_seqlens`` is not modified.
     ``workspace`` (a uint8 device tensor) is allocated from torch's caching
-    allocator when omitted and splits > 1.
+    allocator when omitted and one is needed.
     """
     torch = _torch()
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
@@ -177,12 +189,19 @@ def decode(
             raise PkvError(PKV_EINVAL, "out must match q")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
+    seqlen_new = 0
+    if k_new is not None or v_new is not None:
+        seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
     desc = make_desc(
         batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
         block_table_stride=block_table.shape[1], dtype=_dtype_code(q.dtype), max_seqlen=max_seqlen, path=path,
         split_tokens=split_tokens, prof_events=prof_events,
     )
-    need = workspace_size(desc, num_splits)
+    lib = _lib.load()
+    if seqlen_new:
+        need = int(lib.pkv_decode_append_workspace_size(ctypes.byref(desc), int(num_splits), seqlen_new))
+    else:
+        need = workspace_size(desc, num_splits)
     if need > 0:
         if workspace is None:
             workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
@@ -190,13 +209,102 @@ def decode(
         desc.workspace_bytes = workspace.numel() * workspace.element_size()
     if stream is None:
         stream = torch.cuda.current_stream(q.device).cuda_stream
-    st = _lib.load().pkv_decode(
+    if seqlen_new:
+        st = lib.pkv_decode_append(
+            q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            block_table.data_ptr(), cache_seqlens.data_ptr(), seqlen_new, float(softmax_scale), int(num_splits),
+            out.data_ptr(), ctypes.byref(desc), stream,
+        )
+        if st != PKV_OK:
+            raise PkvError(st, "pkv_decode_append")
+        return out
+    st = lib.pkv_decode(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(), cache_seqlens.data_ptr(),
         float(softmax_scale), int(num_splits), out.data_ptr(), ctypes.byref(desc), stream,
     )
     if st != PKV_OK:
         raise PkvError(st)
     return out
+
+
+def _check_new_tokens(k_new, v_new, k_cache, batch: int) -> int:
+    """Shape/dtype checks of flash-attn's k / v new-token arguments; returns seqlen_new."""
+    if k_new is None or v_new is None:
+        raise PkvError(PKV_EINVAL, "k and v must be given together")
+    _check_cuda("k", k_new)
+    _check_cuda("v", v_new)
+    _, _, Hk, D = k_cache.shape
+    if k_new.dim() != 4 or k_new.shape != v_new.shape or k_new.shape[0] != batch or tuple(k_new.shape[2:]) != (Hk, D):
+        raise PkvError(PKV_EINVAL, "k / v must both be [B, seqlen_new, Hk, D]")
+    if k_new.dtype != k_cache.dtype or v_new.dtype != k_cache.dtype:
+        raise PkvError(PKV_EINVAL, "k / v must have the caches' dtype")
+    return int(k_new.shape[1])
+
+
+def append_kv(k_new, v_new, k_cache, v_cache, block_table, cache_seqlens, *, stream=None) -> None:
+    """Write ``k_new`` / ``v_new`` ([B, seqlen_new, Hk, D]) into the paged caches in place.
+
+    Token j of row b lands at position ``max(cache_seqlens[b], 0) + j`` of the
+    row (slot ``pos % P`` of page ``block_table[b, pos // P]``); positions past
+    the block-table row and out-of-range page ids are skipped.  ``cache_seqlens``
+    is not modified.  The copy flash-attn's ``flash_attn_with_kvcache(k=, v=)``
+    makes before attending.
+    """
+    torch = _torch()
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
+                    ("cache_seqlens", cache_seqlens)):
+        _check_cuda(name, t)
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or k_cache.dtype != v_cache.dtype:
+        raise PkvError(PKV_EINVAL, "k_cache / v_cache must both be [num_pages, P, Hk, D]")
+    if block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32 or block_table.dim() != 2:
+        raise PkvError(PKV_EINVAL, "block_table [B, stride] and cache_seqlens [B] must be int32")
+    B = block_table.shape[0]
+    if cache_seqlens.numel() != B:
+        raise PkvError(PKV_EINVAL, "cache_seqlens must have B entries")
+    seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
+    num_pages, P, Hk, D = k_cache.shape
+    desc = make_desc(batch=B, num_heads=Hk, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
+                     block_table_stride=block_table.shape[1], dtype=_dtype_code(k_cache.dtype))
+    if stream is None:
+        stream = torch.cuda.current_stream(k_cache.device).cuda_stream
+    st = _lib.load().pkv_append_kv(
+        k_new.data_ptr(), v_new.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_table.data_ptr(),
+        cache_seqlens.data_ptr(), seqlen_new, ctypes.byref(desc), stream,
+    )
+    if st != PKV_OK:
+        raise PkvError(st, "pkv_append_kv")
+
+
+def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *, stream=None) -> None:
+    """Write token rows ``key`` / ``value`` ([num_tokens, Hk, D]) to flat cache slots in place.
+
+    ``slot_mapping[i] = page * P + slot`` (int64); a negative slot is padding and
+    is skipped, slots past the cache are not written.  Same cache layout as the
+    decode ([num_pages, P, Hk, D]).
+    """
+    torch = _torch()
+    for name, t in (("key", key), ("value", value), ("key_cache", key_cache), ("value_cache", value_cache),
+                    ("slot_mapping", slot_mapping)):
+        _check_cuda(name, t)
+    if key_cache.dim() != 4 or key_cache.shape != value_cache.shape or key_cache.dtype != value_cache.dtype:
+        raise PkvError(PKV_EINVAL, "key_cache / value_cache must both be [num_pages, P, Hk, D]")
+    num_pages, P, Hk, D = key_cache.shape
+    if key.dim() != 3 or key.shape != value.shape or tuple(key.shape[1:]) != (Hk, D):
+        raise PkvError(PKV_EINVAL, "key / value must both be [num_tokens, Hk, D]")
+    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype:
+        raise PkvError(PKV_EINVAL, "key / value must have the caches' dtype")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != key.shape[0]:
+        raise PkvError(PKV_EINVAL, "slot_mapping must be int64 with one entry per token")
+    desc = make_desc(batch=0, num_heads=0, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
+                     block_table_stride=0, dtype=_dtype_code(key_cache.dtype))
+    if stream is None:
+        stream = torch.cuda.current_stream(key_cache.device).cuda_stream
+    st = _lib.load().pkv_reshape_and_cache(
+        key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(),
+        int(key.shape[0]), ctypes.byref(desc), stream,
+    )
+    if st != PKV_OK:
+        raise PkvError(st, "pkv_reshape_and_cache")
 
 
 def flash_attn_with_kvcache(
@@ -223,11 +331,15 @@ def flash_attn_with_kvcache(
     """Paged decode with the reference evaluator's call signature (eval:232-247).
 
     Supported: seqlen_q = 1, paged caches with ``block_table`` and
-    ``cache_seqlens``; ``causal`` is accepted (it is a no-op for one query
-    token at the end of the cache).  Anything else raises PkvError(PKV_EUNSUPPORTED).
+    ``cache_seqlens`` (a tensor or one int for every row), and new tokens
+    ``k`` / ``v`` [B, seqlen_new, Hk, D], written into the caches in place
+    before the attention, which then covers ``cache_seqlens + seqlen_new``
+    tokens (flash-attn 2.6.3).  ``causal`` is accepted (it is a no-op for one
+    query token at the end of the cache).  Anything else raises
+    PkvError(PKV_EUNSUPPORTED).
     """
-    if k is not None or v is not None or rotary_cos is not None or rotary_sin is not None:
-        raise PkvError(PKV_EUNSUPPORTED, "appending new K/V inside the call")
+    if rotary_cos is not None or rotary_sin is not None:
+        raise PkvError(PKV_EUNSUPPORTED, "rotary embedding of the new K")
     if cache_batch_idx is not None or cache_leftpad is not None:
         raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
     if tuple(window_size) != (-1, -1) or softcap or alibi_slopes is not None:
@@ -238,7 +350,14 @@ def flash_attn_with_kvcache(
         raise PkvError(PKV_EUNSUPPORTED, "only the paged layout (block_table + cache_seqlens) is implemented")
     if q.shape[1] != 1:
         raise PkvError(PKV_EUNSUPPORTED, "seqlen_q > 1")
-    return decode(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits)
+    if isinstance(cache_seqlens, int):
+        torch = _torch()
+        cache_seqlens = torch.full((q.shape[0],), cache_seqlens, dtype=torch.int32, device=q.device)
+    if k is not None:
+        k = k.contiguous()
+    if v is not None:
+        v = v.contiguous()
+    return decode(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k, v_new=v)
 
 
 def run_kernel(

@@ -43,6 +43,10 @@ EXPORTS = {
     "pkv_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "run_kernel": (None, [ctypes.c_void_p] * 4 + [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 9),
     "pkv_last_status": (ctypes.c_int, []),
+    "pkv_append_kv": (ctypes.c_int, None),
+    "pkv_reshape_and_cache": (ctypes.c_int, None),
+    "pkv_decode_append": (ctypes.c_int, None),
+    "pkv_decode_append_workspace_size": (ctypes.c_size_t, None),
 }
 
 
@@ -106,6 +110,28 @@ def load() -> ctypes.CDLL:
     lib.pkv_decode_schedule.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_path.restype = ctypes.c_int
     lib.pkv_decode_path.argtypes = [desc_p]
+    vp = ctypes.c_void_p
+    lib.pkv_append_kv.restype = ctypes.c_int
+    lib.pkv_append_kv.argtypes = [
+        vp, vp, vp, vp,                                     # k_new, v_new, k_cache, v_cache
+        vp, vp, ctypes.c_int64,                             # block_table, cache_seqlens, seqlen_new
+        desc_p, vp,                                         # desc, stream
+    ]
+    lib.pkv_reshape_and_cache.restype = ctypes.c_int
+    lib.pkv_reshape_and_cache.argtypes = [
+        vp, vp, vp, vp,                                     # key, value, k_cache, v_cache
+        vp, ctypes.c_int64,                                 # slot_mapping, num_tokens
+        desc_p, vp,                                         # desc, stream
+    ]
+    lib.pkv_decode_append.restype = ctypes.c_int
+    lib.pkv_decode_append.argtypes = [
+        vp, vp, vp, vp, vp,                                 # q, k_new, v_new, k_cache, v_cache
+        vp, vp, ctypes.c_int64,                             # block_table, cache_seqlens, seqlen_new
+        ctypes.c_float, ctypes.c_int, vp,                   # softmax_scale, num_splits, out
+        desc_p, vp,                                         # desc, stream
+    ]
+    lib.pkv_decode_append_workspace_size.restype = ctypes.c_size_t
+    lib.pkv_decode_append_workspace_size.argtypes = [desc_p, ctypes.c_int, ctypes.c_int64]
     for name in ("pkv_strerror", "run_kernel", "pkv_last_status"):
         res, args = EXPORTS[name]
         fn = getattr(lib, name)

@@ -23,7 +23,7 @@ LIB_PATH = LIB_DIR / "libpkv_decode.so"
 ORACLE_DIR = REPO_ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "libpkv_oracle.so"
 
-SOURCES = ["pkv_partition.hip", "pkv_combine.hip", "pkv_api.cpp"]
+SOURCES = ["pkv_partition.hip", "pkv_combine.hip", "pkv_append.hip", "pkv_api.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

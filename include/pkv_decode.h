@@ -129,6 +129,61 @@ int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits);
 /* Kernel family pkv_decode will use for this desc (resolves PKV_PATH_AUTO). */
 int pkv_decode_path(const pkv_decode_desc* desc);
 
+/*
+ * Paged KV-cache append: writes seqlen_new new tokens per row into the cache,
+ * token j of row b at position max(cache_seqlens[b], 0) + j, i.e. slot
+ * (pos % P) of page block_table[b][pos / P].
+ *   k_new, v_new  [B, seqlen_new, Hk, D]  16-bit (desc->dtype), contiguous, 16-byte aligned
+ * desc is the attention calls' descriptor (it must pass the same checks);
+ * the append uses its batch, num_heads_k, head_dim, page_size, num_pages,
+ * block_table_stride and dtype, and ignores the workspace.  Positions at or past
+ * block_table_stride * P and page ids outside [0, num_pages) are not written.
+ * cache_seqlens is read, never updated (the caller advances it, as with
+ * flash-attn).  Replaces the in-kernel append of flash-attn 2.6.3's
+ * flash_attn_with_kvcache(k=, v=), which the reference's evaluator passes as
+ * None (scripts/evaluate_flashattn_submission.py:236-237).
+ * Asynchronous on `stream`.
+ */
+int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                  const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_new,
+                  const pkv_decode_desc* desc, void* stream);
+
+/*
+ * Paged KV-cache append by flat slot: token row i of key / value
+ * ([num_tokens, Hk, D], 16-bit, contiguous) goes to slot_mapping[i] =
+ * page * P + slot of the [num_pages, P, Hk, D] caches; a negative slot is
+ * padding and is skipped, a slot >= num_pages * P is not written.  The
+ * slot-mapped form of the same copy (vLLM's reshape_and_cache_flash); the
+ * reference has no counterpart (its evaluator passes no new tokens,
+ * scripts/evaluate_flashattn_submission.py:236-237).  Only desc's
+ * num_heads_k, head_dim, page_size, num_pages, dtype and path are read (and
+ * checked as pkv_decode checks them); the row-shaped fields may be 0.
+ */
+int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int64_t num_tokens, const pkv_decode_desc* desc,
+                          void* stream);
+
+/*
+ * flash_attn_with_kvcache(q, k_cache, v_cache, k=k_new, v=v_new,
+ * cache_seqlens=, block_table=) for seqlen_q = 1: appends k_new / v_new as
+ * pkv_append_kv does, then attends over the first
+ * max(cache_seqlens[b], 0) + seqlen_new tokens of each row (flash-attn 2.6.3
+ * semantics; the reference's evaluator passes k = v = None,
+ * scripts/evaluate_flashattn_submission.py:236-237).  desc->max_seqlen, when
+ * set, bounds cache_seqlens before the append.  The workspace must hold
+ * pkv_decode_append_workspace_size(desc, num_splits, seqlen_new) bytes (it
+ * always holds the per-row lengths, so it is never NULL); prof_events, when
+ * set, time the attention kernels as in pkv_decode.  seqlen_new == 0 is
+ * pkv_decode.
+ */
+int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_new,
+                      float softmax_scale, int num_splits, void* out, const pkv_decode_desc* desc,
+                      void* stream);
+
+/* Bytes of workspace pkv_decode_append needs. */
+size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new);
+
 /* Human-readable name of a status code. */
 const char* pkv_strerror(int status);
 

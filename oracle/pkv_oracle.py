@@ -3,7 +3,9 @@
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, as the checker (or the timed CPU baseline).
 16-bit tensors are numpy uint16 bit patterns; dtype 0 = fp16, 1 = bf16.
-Function-by-function reference citations are in pkv_oracle.c.
+Function-by-function reference citations of the attention are in
+pkv_oracle.c; the paged KV-cache append (numpy, at the end of this file) cites
+its sources there.
 """
 from __future__ import annotations
 
@@ -161,3 +163,59 @@ def f32_to_bits(x: np.ndarray, dtype: int) -> np.ndarray:
         r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
         return r
     return x.astype(np.float16).view(np.uint16)
+
+
+# ------------------------------------------------------------------ paged KV-cache append (numpy)
+#
+# The reference's evaluator calls flash_attn_with_kvcache with k = v = None
+# (scripts/evaluate_flashattn_submission.py:236-237), so its append step comes
+# from the pinned dependency flash-attn 2.6.3 (setup/pip_full_list.txt:54):
+# "k_cache and v_cache are updated in place with the new values from k and v,
+# starting at the indices specified by cache_seqlens", and the attention then
+# covers cache_seqlens + seqlen_new tokens.  The slot form restates vLLM's
+# reshape_and_cache_flash (flat slot = page * P + slot, negative = padding).
+
+def append_positions(block_table, seqlens, seqlen_new, page_size, num_pages):
+    """(page, slot, keep) [B, seqlen_new] for token j of row b at position max(seqlens[b], 0) + j.
+
+    keep is False where the position is past the block-table row or the page id
+    is outside [0, num_pages)."""
+    bt = np.asarray(block_table, dtype=np.int64)
+    B, stride = bt.shape
+    pos = np.maximum(np.asarray(seqlens, dtype=np.int64), 0)[:, None] + np.arange(seqlen_new, dtype=np.int64)[None, :]
+    keep = pos < stride * page_size
+    col = np.where(keep, pos // page_size, 0)
+    page = bt[np.arange(B)[:, None], col]
+    keep &= (page >= 0) & (page < num_pages)
+    return page, pos % page_size, keep
+
+
+def append_kv(k_cache, v_cache, block_table, seqlens, k_new, v_new, inplace=False):
+    """The caches after appending k_new / v_new [B, n, Hk, D] (flash-attn 2.6.3 k= / v=);
+    updated copies, or the given arrays when inplace."""
+    kc = k_cache if inplace else np.array(k_cache, copy=True)
+    vc = v_cache if inplace else np.array(v_cache, copy=True)
+    B, n = k_new.shape[:2]
+    page, slot, keep = append_positions(block_table, seqlens, n, k_cache.shape[1], k_cache.shape[0])
+    bi, ji = np.nonzero(keep)
+    kc[page[keep], slot[keep]] = k_new[bi, ji]
+    vc[page[keep], slot[keep]] = v_new[bi, ji]
+    return kc, vc
+
+
+def reshape_and_cache(k_cache, v_cache, key, value, slot_mapping, inplace=False):
+    """The caches after writing token rows key / value [T, Hk, D] to flat slots; updated
+    copies, or the given arrays when inplace."""
+    kc = k_cache if inplace else np.array(k_cache, copy=True)
+    vc = v_cache if inplace else np.array(v_cache, copy=True)
+    num_pages, P = k_cache.shape[:2]
+    slots = np.asarray(slot_mapping, dtype=np.int64)
+    keep = (slots >= 0) & (slots < num_pages * P)
+    kc.reshape(num_pages * P, *k_cache.shape[2:])[slots[keep]] = key[keep]
+    vc.reshape(num_pages * P, *v_cache.shape[2:])[slots[keep]] = value[keep]
+    return kc, vc
+
+
+def appended_seqlens(seqlens, seqlen_new):
+    """Row lengths the attention covers after an append of seqlen_new tokens."""
+    return (np.maximum(np.asarray(seqlens, dtype=np.int64), 0) + seqlen_new).astype(np.int32)

@@ -191,3 +191,68 @@ def test_reserved_field_must_be_zero():
     d = base_desc()
     d.reserved = 1
     assert pagedkv.num_splits_for(d, 0) == 0
+
+
+# ------------------------------------------------------------------ paged KV-cache append
+
+def test_append_entry_points_reject_bad_arguments_before_any_launch():
+    lib = _lib.load()
+    d = base_desc()
+    p = ctypes.c_void_p(4096)
+    odd = ctypes.c_void_p(4104)
+    E = pagedkv.PKV_EINVAL
+    assert lib.pkv_append_kv(None, p, p, p, p, p, 1, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, odd, p, p, p, 1, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, p, p, None, p, 1, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, p, p, p, None, 1, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, p, p, p, p, -1, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, p, p, p, p, 1, None, None) == E
+    bad = base_desc(head_dim=96)
+    assert lib.pkv_append_kv(p, p, p, p, p, p, 1, ctypes.byref(bad), None) == pagedkv.PKV_EUNSUPPORTED
+    assert lib.pkv_reshape_and_cache(p, p, p, p, None, 4, ctypes.byref(d), None) == E
+    assert lib.pkv_reshape_and_cache(p, odd, p, p, p, 4, ctypes.byref(d), None) == E
+    assert lib.pkv_reshape_and_cache(p, p, p, p, p, -4, ctypes.byref(d), None) == E
+    assert lib.pkv_decode_append(p, p, None, p, p, p, p, 1, 0.1, 0, p, ctypes.byref(d), None) == E
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, -2, 0.1, 0, p, ctypes.byref(d), None) == E
+
+
+def test_slot_form_needs_only_the_cache_geometry():
+    """The row-shaped fields of the descriptor may be 0 for the slot form: with zero
+    tokens it validates and returns without launching anything."""
+    lib = _lib.load()
+    d = pagedkv.make_desc(batch=0, num_heads=0, num_heads_k=8, head_dim=128, page_size=16, num_pages=100,
+                          block_table_stride=0, dtype=pagedkv.PKV_DTYPE_F16)
+    p = ctypes.c_void_p(4096)
+    assert lib.pkv_reshape_and_cache(p, p, p, p, p, 0, ctypes.byref(d), None) == pagedkv.PKV_OK
+    d.page_size = 24
+    assert lib.pkv_reshape_and_cache(p, p, p, p, p, 0, ctypes.byref(d), None) == pagedkv.PKV_EUNSUPPORTED
+
+
+def test_decode_append_workspace_holds_row_lengths_then_the_longer_rows_partials():
+    lib = _lib.load()
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for max_seqlen, n, splits in ((4096, 1, 0), (4000, 96, 0), (4096, 3, 8), (0, 5, 0), (100, 2, 1)):
+        d = base_desc(max_seqlen=max_seqlen)
+        longer = base_desc(max_seqlen=max_seqlen + n if max_seqlen else 0)
+        got = lib.pkv_decode_append_workspace_size(ctypes.byref(d), splits, n)
+        assert got == align(32 * 4) + pagedkv.workspace_size(longer, splits)
+    d = base_desc()
+    assert lib.pkv_decode_append_workspace_size(ctypes.byref(d), 0, 0) == pagedkv.workspace_size(d, 0)
+    assert lib.pkv_decode_append_workspace_size(ctypes.byref(d), 0, -1) == 0
+
+
+def test_decode_append_without_workspace_is_reported_before_the_cache_is_written():
+    lib = _lib.load()
+    d = base_desc()
+    p = ctypes.c_void_p(4096)
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, 1, 0.1, 1, p, ctypes.byref(d), None) == \
+        pagedkv.PKV_ENOWORKSPACE
+    # Room for the row lengths but not for the partials of a forced split.
+    d.workspace = 4096
+    d.workspace_bytes = 256
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, 1, 0.1, 4, p, ctypes.byref(d), None) == \
+        pagedkv.PKV_ENOWORKSPACE
+    # Attention-side argument errors surface before the append too.
+    d.workspace_bytes = lib.pkv_decode_append_workspace_size(ctypes.byref(d), 4, 1)
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, 1, float("nan"), 4, p, ctypes.byref(d), None) == \
+        pagedkv.PKV_EINVAL

@@ -1,0 +1,215 @@
+"""GPU parity of the paged KV-cache append (through the C ABI) against the CPU oracle.
+
+Caches are compared bit-exactly (the append is a copy); the attention after an
+append (pkv_decode_append, flash_attn_with_kvcache(k=, v=)) is held to the
+decode tolerances against the fp64 oracle over the oracle-appended cache, and
+must equal append followed by a plain decode bit-for-bit.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import pkv_oracle as po
+from conftest import gpu_available, rand_bits
+from test_gpu_parity import TOL, announce, from_dev, to_dev, torch_mod
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
+
+
+def make_append_case(rng, *, B, H, Hk, D, P, lens, n, dtype, stride_extra=0, pool_extra=3):
+    """Rows with room for n more tokens: distinct scattered pages, unused entries -1."""
+    lens = np.asarray(lens, dtype=np.int32)
+    pages = (np.maximum(lens, 0) + n + P - 1) // P
+    stride = int(pages.max()) + stride_extra
+    pool = int(pages.sum()) + pool_extra
+    perm = rng.permutation(pool).astype(np.int32)
+    bt = np.full((B, max(stride, 1)), -1, dtype=np.int32)
+    at = 0
+    for b in range(B):
+        bt[b, :pages[b]] = perm[at:at + pages[b]]
+        at += pages[b]
+    q = rand_bits(rng, (B, 1, H, D), dtype)
+    kc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    vc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    nk = rand_bits(rng, (B, n, Hk, D), dtype)
+    nv = rand_bits(rng, (B, n, Hk, D), dtype)
+    return q, kc, vc, bt, lens, nk, nv
+
+
+def i32(a):
+    torch = torch_mod()
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).cuda()
+
+
+APPEND = [
+    # B, Hk, D, P, lens, n, dtype
+    (4, 8, 128, 64, [100, 0, 63, 64], 1, 1),
+    (3, 2, 64, 16, [5, 16, 31], 7, 0),
+    (2, 1, 256, 1, [3, 0], 5, 0),
+    (5, 4, 128, 32, [1, 2, 33, 95, 200], 40, 1),
+    (1, 16, 64, 1024, [1000], 50, 1),
+]
+
+
+@pytest.mark.parametrize("B,Hk,D,P,lens,n,dtype", APPEND)
+def test_append_kv_bit_exact(rng, B, Hk, D, P, lens, n, dtype):
+    import pagedkv
+
+    announce("append_kv", B, Hk, D, P, lens, n, dtype)
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=Hk, Hk=Hk, D=D, P=P, lens=lens, n=n, dtype=dtype)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    dk, dv, dsl = to_dev(kc, dtype), to_dev(vc, dtype), i32(sl)
+    pagedkv.append_kv(to_dev(nk, dtype), to_dev(nv, dtype), dk, dv, i32(bt), dsl)
+    torch_mod().cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+    np.testing.assert_array_equal(dsl.cpu().numpy(), sl)  # cache_seqlens is read, never written
+
+
+def test_append_kv_skips_out_of_row_positions_and_bad_pages(rng):
+    import pagedkv
+
+    announce("append_kv-edges")
+    Hk, D, P, dtype = 2, 64, 4, 1
+    bt = np.array([[0, 1], [2, 99], [3, -1], [4, 5]], dtype=np.int32)
+    sl = np.array([6, 2, -5, 8], dtype=np.int32)
+    kc = rand_bits(rng, (6, P, Hk, D), dtype)
+    vc = rand_bits(rng, (6, P, Hk, D), dtype)
+    nk = rand_bits(rng, (4, 4, Hk, D), dtype)
+    nv = rand_bits(rng, (4, 4, Hk, D), dtype)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    dk, dv = to_dev(kc, dtype), to_dev(vc, dtype)
+    pagedkv.append_kv(to_dev(nk, dtype), to_dev(nv, dtype), dk, dv, i32(bt), i32(sl))
+    torch_mod().cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_reshape_and_cache_bit_exact_with_padding(rng, dtype):
+    import pagedkv
+
+    torch = torch_mod()
+    announce("reshape_and_cache", dtype)
+    pool, P, Hk, D, T = 40, 16, 4, 128, 300
+    kc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    vc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    key = rand_bits(rng, (T, Hk, D), dtype)
+    val = rand_bits(rng, (T, Hk, D), dtype)
+    slots = rng.permutation(pool * P)[:T].astype(np.int64)
+    slots[::7] = -1                  # padding tokens
+    slots[3] = pool * P + 5          # past the cache: skipped
+    want_k, want_v = po.reshape_and_cache(kc, vc, key, val, slots)
+    dk, dv = to_dev(kc, dtype), to_dev(vc, dtype)
+    pagedkv.reshape_and_cache_flash(to_dev(key, dtype), to_dev(val, dtype), dk, dv,
+                                    torch.from_numpy(slots).cuda())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+
+
+def test_reshape_and_cache_prefill_size_round_trip():
+    """A prefill-sized write (256K tokens, 1 GiB of K and V): every token reads back from its
+    slot through torch indexing, and slots not named keep their old contents."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("reshape_and_cache-prefill")
+    pool, P, Hk, D, T = 8704, 32, 8, 128, 1 << 18
+    g = torch.Generator(device="cuda").manual_seed(0)
+    kc = torch.randn((pool, P, Hk, D), device="cuda", dtype=torch.bfloat16, generator=g)
+    vc = torch.randn((pool, P, Hk, D), device="cuda", dtype=torch.bfloat16, generator=g)
+    k0, v0 = kc.clone(), vc.clone()
+    key = torch.randn((T, Hk, D), device="cuda", dtype=torch.bfloat16, generator=g)
+    val = torch.randn((T, Hk, D), device="cuda", dtype=torch.bfloat16, generator=g)
+    slots = torch.randperm(pool * P, device="cuda", generator=g)[:T]
+    pagedkv.reshape_and_cache_flash(key, val, kc, vc, slots)
+    torch.cuda.synchronize()
+    flat_k, flat_v = kc.view(pool * P, Hk, D), vc.view(pool * P, Hk, D)
+    assert torch.equal(flat_k[slots].view(torch.int16), key.view(torch.int16))
+    assert torch.equal(flat_v[slots].view(torch.int16), val.view(torch.int16))
+    untouched = torch.ones(pool * P, dtype=torch.bool, device="cuda")
+    untouched[slots] = False
+    assert torch.equal(flat_k[untouched].view(torch.int16), k0.view(pool * P, Hk, D)[untouched].view(torch.int16))
+    assert torch.equal(flat_v[untouched].view(torch.int16), v0.view(pool * P, Hk, D)[untouched].view(torch.int16))
+
+
+DECODE_APPEND = [
+    # B, H, Hk, D, P, lens, n, dtype
+    (4, 32, 8, 128, 64, [511, 0, 64, 1000], 1, 1),
+    (3, 8, 2, 64, 16, [0, 1, 47], 3, 0),
+    (2, 16, 1, 256, 16, [100, 9], 2, 0),
+    (5, 64, 8, 128, 32, [1, 2, 33, 95, 200], 1, 1),
+    (2, 12, 4, 128, 8, [300, 41], 17, 1),
+]
+
+
+@pytest.mark.parametrize("splits", [0, 1, 4])
+@pytest.mark.parametrize("B,H,Hk,D,P,lens,n,dtype", DECODE_APPEND)
+def test_decode_append_matches_oracle(rng, splits, B, H, Hk, D, P, lens, n, dtype):
+    import pagedkv
+
+    torch = torch_mod()
+    announce("decode_append", B, H, Hk, D, P, lens, n, dtype, "splits", splits)
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, lens=lens, n=n, dtype=dtype)
+    scale = 1.0 / math.sqrt(D)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    want = po.decode_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, n), scale, dtype)
+    dk, dv, dsl = to_dev(kc, dtype), to_dev(vc, dtype), i32(sl)
+    out = pagedkv.flash_attn_with_kvcache(to_dev(q, dtype), dk, dv, to_dev(nk, dtype), to_dev(nv, dtype),
+                                          cache_seqlens=dsl, block_table=i32(bt), softmax_scale=scale,
+                                          num_splits=splits)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+    np.testing.assert_array_equal(dsl.cpu().numpy(), sl)
+    got = po.bits_to_f32(from_dev(out), dtype)
+    assert np.max(np.abs(got - want)) < TOL[dtype]
+
+
+@pytest.mark.parametrize("splits", [0, 1])
+def test_decode_append_equals_append_then_decode(rng, splits):
+    """One call (append + attention over the longer rows) gives exactly the bits of the two
+    steps done apart."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("decode_append-vs-two-steps", splits)
+    B, H, Hk, D, P, n, dtype = 6, 32, 8, 128, 64, 2, 1
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=H, Hk=Hk, D=D, P=P,
+                                                 lens=[0, 1, 63, 64, 700, 2000], n=n, dtype=dtype)
+    dq, dnk, dnv, dbt = to_dev(q, dtype), to_dev(nk, dtype), to_dev(nv, dtype), i32(bt)
+    k1, v1 = to_dev(kc, dtype), to_dev(vc, dtype)
+    one = pagedkv.decode(dq, k1, v1, dbt, i32(sl), None, splits, k_new=dnk, v_new=dnv)
+    k2, v2 = to_dev(kc, dtype), to_dev(vc, dtype)
+    pagedkv.append_kv(dnk, dnv, k2, v2, dbt, i32(sl))
+    two = pagedkv.decode(dq, k2, v2, dbt, i32(po.appended_seqlens(sl, n)), None, splits)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(one), from_dev(two))
+    np.testing.assert_array_equal(from_dev(k1), from_dev(k2))
+
+
+def test_decode_append_int_seqlens_and_zero_new_tokens(rng):
+    """flash-attn accepts one int for every row's cache length; seqlen_new = 0 is a plain decode."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("decode_append-int-seqlens")
+    B, H, Hk, D, P, dtype = 3, 8, 2, 64, 16, 0
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, lens=[40, 40, 40], n=2,
+                                                 dtype=dtype)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    want = po.decode_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, 2), 0.125, dtype)
+    dk, dv = to_dev(kc, dtype), to_dev(vc, dtype)
+    out = pagedkv.flash_attn_with_kvcache(to_dev(q, dtype), dk, dv, to_dev(nk, dtype), to_dev(nv, dtype),
+                                          cache_seqlens=40, block_table=i32(bt), softmax_scale=0.125)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(po.bits_to_f32(from_dev(out), dtype) - want)) < TOL[dtype]
+    empty = to_dev(nk[:, :0], dtype)
+    out0 = pagedkv.flash_attn_with_kvcache(to_dev(q, dtype), dk, dv, empty, empty, cache_seqlens=42,
+                                           block_table=i32(bt), softmax_scale=0.125)
+    torch.cuda.synchronize()
+    assert np.max(np.abs(po.bits_to_f32(from_dev(out0), dtype) - want)) < TOL[dtype]
