@@ -340,6 +340,15 @@ bool append_fits(const Resolved& r, int64_t seqlen_new) {
     return seqlen_new <= INT32_MAX && r.B * seqlen_new <= (int64_t{1} << 40) && r.Hk * r.D / 8 <= INT32_MAX;
 }
 
+// Profiling events of a standalone append: desc->prof_events[0] and [1].
+pkv::LaunchEvents append_events(const pkv_decode_desc* d) {
+    const hipEvent_t* ev = static_cast<const hipEvent_t*>(d->prof_events);
+    if (ev == nullptr) {
+        return {};
+    }
+    return {ev[0], ev[1]};
+}
+
 // Workspace of pkv_decode_append: the per-row lengths after the append, then
 // the attention's own workspace for the longer rows.
 pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
@@ -428,7 +437,9 @@ int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_c
     a.block_table = block_table;
     a.seqlens = cache_seqlens;
     a.n_new = static_cast<int32_t>(seqlen_new);
-    return pkv::launch_append(a, static_cast<hipStream_t>(stream), {}) == hipSuccess ? PKV_OK : PKV_ELAUNCH;
+    return pkv::launch_append(a, static_cast<hipStream_t>(stream), append_events(desc)) == hipSuccess
+               ? PKV_OK
+               : PKV_ELAUNCH;
 }
 
 int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
@@ -459,7 +470,9 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, voi
     pkv::AppendParams a = append_params(r, &g, key, value, k_cache, v_cache, num_tokens);
     a.slot_mapping = slot_mapping;
     a.n_new = 1;
-    return pkv::launch_append(a, static_cast<hipStream_t>(stream), {}) == hipSuccess ? PKV_OK : PKV_ELAUNCH;
+    return pkv::launch_append(a, static_cast<hipStream_t>(stream), append_events(desc)) == hipSuccess
+               ? PKV_OK
+               : PKV_ELAUNCH;
 }
 
 size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new) {

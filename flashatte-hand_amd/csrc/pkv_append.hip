@@ -3,7 +3,8 @@
 // Writes new tokens' K and V rows into their page slots.  A pure copy: every
 // byte of the new-token tensors is read once and written once into the cache,
 // so the kernel is HBM-bound at 4 bytes moved per 16-bit element of K and V
-// each.  One 16-byte chunk of K and one of V per thread, grid-strided.
+// each.  Each thread moves kAppendUnroll 16-byte chunks of K and of V per
+// grid-strided pass, all loads issued before the stores.
 //
 // Two index sources for the destination slot of token row i:
 //  - block table (flash-attn 2.6.3 flash_attn_with_kvcache with k / v given;
@@ -25,46 +26,93 @@ namespace pkv {
 
 constexpr int kAppendThreads = 256;
 
+// Chunks per thread per pass: their loads are all issued before any store.
+// 1, 2, 4 and 8 measured within 3 % of each other on a 560 MB append; 2 was best.
+constexpr int kAppendUnroll = 2;
+
 // Grid cap: enough workgroups to keep every CU's memory pipeline full; larger
-// copies loop.
+// copies loop.  8 and unlimited measured the same as 32 per CU.
 constexpr int64_t kAppendMaxGroups = int64_t{kComputeUnits} * 32;
+
+// Destination chunk of flat chunk x (token row x / chunks), or -1 when the
+// token is not written.  The block-table form also records the row's new
+// length once per row.
+template <bool SLOTS>
+__device__ __forceinline__ int64_t append_dst(const AppendParams& p, int64_t x) {
+    int64_t i;
+    int32_t c;
+    if (x <= INT32_MAX) {
+        const uint32_t xi = static_cast<uint32_t>(x);
+        const uint32_t ii = xi / static_cast<uint32_t>(p.chunks);
+        i = ii;
+        c = static_cast<int32_t>(xi - ii * static_cast<uint32_t>(p.chunks));
+    } else {
+        i = x / p.chunks;
+        c = static_cast<int32_t>(x - i * p.chunks);
+    }
+    int64_t slot;
+    if constexpr (SLOTS) {
+        slot = p.slot_mapping[i];
+        if (slot < 0 || slot >= p.num_slots) {
+            return -1;
+        }
+    } else {
+        const int32_t b = static_cast<int32_t>(i / p.n_new);
+        const int32_t j = static_cast<int32_t>(i - static_cast<int64_t>(b) * p.n_new);
+        const int64_t base = max(p.seqlens[b], 0);
+        if (p.seqlens_out != nullptr && j == 0 && c == 0) {
+            p.seqlens_out[b] = static_cast<int32_t>(min(base + p.n_new, static_cast<int64_t>(INT32_MAX)));
+        }
+        const int64_t pos = base + j;
+        if (pos >= p.row_cap) {
+            return -1;
+        }
+        const int32_t page =
+            p.block_table[static_cast<int64_t>(b) * p.bt_stride + static_cast<int32_t>(pos >> p.page_shift)];
+        if (page < 0 || page >= p.num_pages) {
+            return -1;
+        }
+        slot = (static_cast<int64_t>(page) << p.page_shift) | (pos & ((int64_t{1} << p.page_shift) - 1));
+    }
+    return slot * p.chunks + c;
+}
 
 template <bool SLOTS>
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendParams p) {
+    constexpr int U = kAppendUnroll;
     const int64_t total = p.tokens * p.chunks;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * kAppendThreads;
-    for (int64_t x = static_cast<int64_t>(blockIdx.x) * kAppendThreads + threadIdx.x; x < total; x += step) {
-        const int64_t i = x / p.chunks;
-        const int32_t c = static_cast<int32_t>(x - i * p.chunks);
-        int64_t slot;
-        if constexpr (SLOTS) {
-            slot = p.slot_mapping[i];
-            if (slot < 0 || slot >= p.num_slots) {
-                continue;
+    const int64_t span = int64_t{kAppendThreads} * U;
+    const u32x4* k_new = reinterpret_cast<const u32x4*>(p.k_new);
+    const u32x4* v_new = reinterpret_cast<const u32x4*>(p.v_new);
+    u32x4* k_cache = reinterpret_cast<u32x4*>(p.k_cache);
+    u32x4* v_cache = reinterpret_cast<u32x4*>(p.v_cache);
+    for (int64_t x0 = static_cast<int64_t>(blockIdx.x) * span + threadIdx.x; x0 < total;
+         x0 += static_cast<int64_t>(gridDim.x) * span) {
+        u32x4 kx[U];
+        u32x4 vx[U];
+        int64_t dst[U];
+        // The source reads depend only on x: issue them first, then the index loads.
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t x = x0 + int64_t{u} * kAppendThreads;
+            if (x < total) {
+                kx[u] = __builtin_nontemporal_load(k_new + x);
+                vx[u] = __builtin_nontemporal_load(v_new + x);
             }
-        } else {
-            const int32_t b = static_cast<int32_t>(i / p.n_new);
-            const int32_t j = static_cast<int32_t>(i - static_cast<int64_t>(b) * p.n_new);
-            const int64_t base = max(p.seqlens[b], 0);
-            if (p.seqlens_out != nullptr && j == 0 && c == 0) {
-                p.seqlens_out[b] = static_cast<int32_t>(min(base + p.n_new, static_cast<int64_t>(INT32_MAX)));
-            }
-            const int64_t pos = base + j;
-            if (pos >= p.row_cap) {
-                continue;
-            }
-            const int32_t page =
-                p.block_table[static_cast<int64_t>(b) * p.bt_stride + static_cast<int32_t>(pos >> p.page_shift)];
-            if (page < 0 || page >= p.num_pages) {
-                continue;
-            }
-            slot = (static_cast<int64_t>(page) << p.page_shift) | (pos & ((int64_t{1} << p.page_shift) - 1));
         }
-        const u32x4 kx = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.k_new) + x);
-        const u32x4 vx = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.v_new) + x);
-        const int64_t dst = slot * p.chunks + c;
-        reinterpret_cast<u32x4*>(p.k_cache)[dst] = kx;
-        reinterpret_cast<u32x4*>(p.v_cache)[dst] = vx;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t x = x0 + int64_t{u} * kAppendThreads;
+            dst[u] = x < total ? append_dst<SLOTS>(p, x) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (dst[u] >= 0) {
+                // Streaming stores: 3-4 % faster than cached ones on a prefill-sized append.
+                __builtin_nontemporal_store(kx[u], k_cache + dst[u]);
+                __builtin_nontemporal_store(vx[u], v_cache + dst[u]);
+            }
+        }
     }
 }
 
@@ -73,7 +121,8 @@ hipError_t launch_append(const AppendParams& p, hipStream_t stream, const Launch
     if (total <= 0) {
         return hipSuccess;
     }
-    const int64_t groups = std::min<int64_t>((total + kAppendThreads - 1) / kAppendThreads, kAppendMaxGroups);
+    const int64_t span = int64_t{kAppendThreads} * kAppendUnroll;
+    const int64_t groups = std::min<int64_t>((total + span - 1) / span, kAppendMaxGroups);
     if (p.slot_mapping != nullptr) {
         launch_kernel(append_kernel<true>, dim3(static_cast<uint32_t>(groups)), dim3(kAppendThreads), 0, stream, ev,
                       p);

@@ -139,7 +139,8 @@ int pkv_decode_path(const pkv_decode_desc* desc);
  * block_table_stride and dtype, and ignores the workspace.  Positions at or past
  * block_table_stride * P and page ids outside [0, num_pages) are not written.
  * cache_seqlens is read, never updated (the caller advances it, as with
- * flash-attn).  Replaces the in-kernel append of flash-attn 2.6.3's
+ * flash-attn).  desc->prof_events, when set, are hipEvent_t[2] recorded by
+ * the copy kernel's dispatch packet as it starts and completes.  Replaces the in-kernel append of flash-attn 2.6.3's
  * flash_attn_with_kvcache(k=, v=), which the reference's evaluator passes as
  * None (scripts/evaluate_flashattn_submission.py:236-237).
  * Asynchronous on `stream`.
@@ -158,6 +159,7 @@ int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_c
  * scripts/evaluate_flashattn_submission.py:236-237).  Only desc's
  * num_heads_k, head_dim, page_size, num_pages, dtype and path are read (and
  * checked as pkv_decode checks them); the row-shaped fields may be 0.
+ * desc->prof_events as for pkv_append_kv.
  */
 int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
                           const int64_t* slot_mapping, int64_t num_tokens, const pkv_decode_desc* desc,
