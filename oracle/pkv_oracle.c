@@ -14,12 +14,21 @@
  *                              split), 782-833 (exp2 online update), 845-864 (lse2)
  *   pkv_oracle_combine(_f32)   best_flashattn_kvcache_decode.cu:956-1037 and
  *                              v11_best_hybrid/flashattn_kvcache_decode_v11_best_hybrid.cu:604-613
+ *   pkv_oracle_attn_f64        the masks the evaluator passes to flash_attn_with_kvcache
+ *                              (scripts/evaluate_flashattn_submission.py:242-245: causal,
+ *                              window_size, alibi_slopes) with the semantics of the pinned
+ *                              flash-attn 2.6.3 (setup/pip_full_list.txt:54): query i of M at
+ *                              position i + L - M; causal keeps keys j <= pos; a window keeps
+ *                              pos - left <= j <= pos + right; ALiBi adds -slope * |pos - j|
+ *                              to the scaled score; a query with no visible key gives 0
  *
  * How each is pinned (tests/test_oracle.py): the dense fp64 result against an
  * independent numpy formula (including the reference's diagnostic seeds),
  * closed forms (K = 0 gives mean(V); one dominant key gives its V row;
  * seqlen 1 copies V), brute-force gathers, page-permutation invariance, and
- * the split algebra against the single-pass result for many split counts.
+ * the split algebra against the single-pass result for many split counts;
+ * the masked form (tests/test_mask_oracle.py) against the pinned decode over
+ * truncated or re-paged rows, and an ALiBi closed form.
  *
  * Two deliberate differences from the reference, both documented in the
  * design notes: the dot product is summed in 8 interleaved fp32 partial sums
@@ -337,6 +346,97 @@ void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const ui
             }
             for (int64_t i = 0; i < D; ++i) {
                 o[i] = acc[i] / denom;
+            }
+        }
+        free(scores);
+        free(qd);
+    }
+}
+
+/* ---------------------------------------------------------------- fp64 dense, several queries, masks */
+
+void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
+                         int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
+                         const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
+                         double* out) {
+    build_f16_table();
+    set_threads(d);
+    const int64_t B = d->batch, H = d->num_heads, D = d->head_dim, M = seqlen_q;
+    const int64_t group = H / d->num_heads_k;
+    const int32_t dt = d->dtype;
+
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+    {
+        int64_t cap = 0;
+        double* scores = NULL;
+        double* qd = (double*)malloc(sizeof(double) * (size_t)D * 2);
+        double* acc = qd + D;
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int64_t row = 0; row < B * M * H; ++row) {
+            /* q / out row (b, i, h) of [B, M, H, D] */
+            const int64_t b = row / (M * H);
+            const int64_t i = (row / H) % M;
+            const int64_t h = row % H;
+            const int64_t kvh = h / group;
+            const int64_t n = row_seqlen(d, cache_seqlens, b);
+            const int64_t pos = i + n - M;
+            const double slope = alibi_slopes ? (double)alibi_slopes[b * alibi_batch_stride + h] : 0.0;
+            double* o = out + row * D;
+            for (int64_t c = 0; c < D; ++c) {
+                o[c] = 0.0;
+                acc[c] = 0.0;
+            }
+            if (n <= 0) {
+                continue;
+            }
+            if (n > cap) {
+                free(scores);
+                cap = n;
+                scores = (double*)malloc(sizeof(double) * (size_t)cap);
+            }
+            for (int64_t c = 0; c < D; ++c) {
+                qd[c] = (double)to_f32(q[row * D + c], dt);
+            }
+            double mx = -INFINITY;
+            for (int64_t t = 0; t < n; ++t) {
+                const int visible = (!causal || t <= pos) && (window_left < 0 || t >= pos - window_left) &&
+                                    (window_right < 0 || t <= pos + window_right);
+                if (!visible) {
+                    scores[t] = -INFINITY;
+                    continue;
+                }
+                const uint16_t* krow = k_cache + token_offset(d, block_table, b, t, kvh);
+                double s = 0.0;
+                for (int64_t c = 0; c < D; ++c) {
+                    s += qd[c] * (double)to_f32(krow[c], dt);
+                }
+                scores[t] = s * softmax_scale - slope * fabs((double)(pos - t));
+                if (scores[t] > mx) {
+                    mx = scores[t];
+                }
+            }
+            if (mx == -INFINITY) {
+                continue; /* no visible key */
+            }
+            double denom = 0.0;
+            for (int64_t t = 0; t < n; ++t) {
+                if (scores[t] == -INFINITY) {
+                    continue;
+                }
+                const double p = exp(scores[t] - mx);
+                denom += p;
+                const uint16_t* vrow = v_cache + token_offset(d, block_table, b, t, kvh);
+                for (int64_t c = 0; c < D; ++c) {
+                    acc[c] += p * (double)to_f32(vrow[c], dt);
+                }
+            }
+            for (int64_t c = 0; c < D; ++c) {
+                o[c] = acc[c] / denom;
             }
         }
         free(scores);

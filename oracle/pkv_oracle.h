@@ -51,6 +51,22 @@ void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const ui
                            const uint16_t* v_cache, const int32_t* block_table,
                            const int32_t* cache_seqlens, double softmax_scale, double* out);
 
+/* Dense fp64 attention with several query tokens per row and masks
+ * (flash-attn 2.6.3 semantics for the arguments the reference's evaluator
+ * passes, scripts/evaluate_flashattn_submission.py:242-245): q and out are
+ * [B, seqlen_q, H, D]; query i of row b sits at position pos = i + L - seqlen_q
+ * (L = the row's clamped length) and sees the keys t < L with
+ * (!causal || t <= pos), (window_left < 0 || t >= pos - window_left) and
+ * (window_right < 0 || t <= pos + window_right); ALiBi (slopes fp32
+ * [B, H] at alibi_slopes[b * alibi_batch_stride + h], NULL = none) adds
+ * -slope * |pos - t| to the scaled score.  A query without a visible key
+ * gives zeros.  out is fp64. */
+void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
+                         int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
+                         const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
+                         double* out);
+
 /* Split-KV partition step (best_flashattn_kvcache_decode.cu:664-697, 782-864):
  * split s of row b covers pages [n*s/S, n*(s+1)/S) of its n valid pages;
  * exp2-domain fp32 online softmax; part_o [B*H*S, D] normalised, part_lse

@@ -68,6 +68,10 @@ def load():
     lib.pkv_oracle_combine.restype = None
     lib.pkv_oracle_combine_f32.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_int, ctypes.c_int64, _f32p]
     lib.pkv_oracle_combine_f32.restype = None
+    lib.pkv_oracle_attn_f64.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
+                                        ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                        ctypes.c_double, _f64p]
+    lib.pkv_oracle_attn_f64.restype = None
     for n in ("pkv_oracle_f16_to_f32", "pkv_oracle_bf16_to_f32"):
         getattr(lib, n).argtypes = [ctypes.c_uint16]
         getattr(lib, n).restype = ctypes.c_float
@@ -114,6 +118,29 @@ def decode_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, threads=
     out = np.empty(q.shape, dtype=np.float64)
     lib.pkv_oracle_decode_f64(ctypes.byref(d), _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16),
                               _c(block_table, np.int32), _c(seqlens, np.int32), float(scale), out)
+    return out
+
+
+def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=False, window=(-1, -1),
+             alibi=None, threads=0):
+    """Dense fp64 attention of q [B, M, H, D] with flash-attn 2.6.3 masks; returns float64 [B, M, H, D].
+
+    alibi: None, fp32 [H] or [B, H] slopes."""
+    lib = load()
+    B, M, H, D = q.shape
+    num_pages, P, Hk, _ = k_cache.shape
+    d = dims(B, H, Hk, D, P, num_pages, block_table.shape[1], dtype, threads)
+    out = np.empty(q.shape, dtype=np.float64)
+    slopes = None
+    stride = 0
+    if alibi is not None:
+        slopes = np.ascontiguousarray(alibi, dtype=np.float32)
+        stride = H if slopes.ndim == 2 else 0
+    lib.pkv_oracle_attn_f64(ctypes.byref(d), _c(q, np.uint16), _c(k_cache, np.uint16), _c(v_cache, np.uint16),
+                            _c(block_table, np.int32), _c(seqlens, np.int32), int(M), int(bool(causal)),
+                            int(window[0]), int(window[1]),
+                            None if slopes is None else slopes.ctypes.data_as(ctypes.c_void_p), int(stride),
+                            float(scale), out)
     return out
 
 
