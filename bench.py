@@ -90,10 +90,17 @@ def load_traffic(cfg_name: str, path_name):
 
 
 def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
+    import numpy as np
+
     from pagedkv.configs import make_config, make_tensors
 
     cfg = make_config(name)
     sets = [make_tensors(cfg, "cuda", seed=cfg.seed + 7919 * i) for i in range(max(1, args.sets))]
+    M = max(1, args.seqlen_q)
+    if M > 1:
+        # Several query tokens per row (speculative-decode verify): q / out [B, M, H, D].
+        for s_ in sets:
+            s_["q"] = torch.randn((cfg.batch, M, cfg.num_heads, cfg.head_dim), device="cuda").to(s_["q"].dtype)
     torch.cuda.synchronize()
     dev = torch.device("cuda")
     stream = torch.cuda.current_stream(dev)
@@ -105,6 +112,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         page_size=cfg.page_size, num_pages=base["k_cache"].shape[0], block_table_stride=cfg.block_table.shape[1],
         dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
         max_seqlen=int(cfg.seqlens.max()), path=args.path, split_tokens=args.split_tokens,
+        seqlen_q=M, causal=args.causal, window_size=tuple(args.window),
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
@@ -157,17 +165,26 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
 
     ms_per_step = total_ms / K
     kv_bytes = cfg.kv_bytes()
+    if args.window[0] >= 0:
+        # A left window leaves each row the keys from L - M - left on.
+        L = cfg.seqlens.clip(min=0).astype(np.int64)
+        span = L - np.clip(L - M - args.window[0], 0, None)
+        kv_bytes = int(span.sum()) * cfg.num_heads_k * D * 2 * cfg.elem_bytes
     # Algorithmic bytes of one partition launch: valid K/V rows + q + block-table entries + seqlens
     # (the output is written by the combine kernel and is not counted here).
     part_alg = cfg.total_bytes() - cfg.batch * cfg.num_heads * D * cfg.elem_bytes
+    part_alg += (M - 1) * cfg.batch * cfg.num_heads * D * cfg.elem_bytes  # the extra query rows
+    part_alg += kv_bytes - cfg.kv_bytes()                                   # window: visible keys only
     part_avg_ms = sum(part_ms) / K
     achieved = part_alg / (part_avg_ms * 1e-3) / 1e9
-    traffic = load_traffic(name, "mfma" if path == pagedkv.PKV_PATH_MFMA else "valu")
+    # The committed counter summary is for the one-query, unmasked decode.
+    plain = M == 1 and tuple(args.window) == (-1, -1)
+    traffic = load_traffic(name, "mfma" if path == pagedkv.PKV_PATH_MFMA else "valu") if plain else None
     res = {
         "config": cfg,
         "ms_per_step": ms_per_step,
         "kv_gbps": kv_bytes / (ms_per_step * 1e-3) / 1e9,
-        "total_gbps": cfg.total_bytes() / (ms_per_step * 1e-3) / 1e9,
+        "total_gbps": (cfg.total_bytes() + kv_bytes - cfg.kv_bytes()) / (ms_per_step * 1e-3) / 1e9,
         "us_p10": percentile(call_ms, 10) * 1e3,
         "us_p50": percentile(call_ms, 50) * 1e3,
         "us_p90": percentile(call_ms, 90) * 1e3,
@@ -378,6 +395,11 @@ def main() -> int:
     ap.add_argument("--json-out", default=None, help="append one JSON line per measured config to this file")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seqlen-q", type=int, default=1,
+                    help="query tokens per row (decode op): > 1 is the speculative-decode verify shape")
+    ap.add_argument("--causal", action="store_true", help="causal mask (decode op, with --seqlen-q > 1)")
+    ap.add_argument("--window", type=int, nargs=2, default=(-1, -1), metavar=("LEFT", "RIGHT"),
+                    help="sliding window (decode op); -1 = unbounded")
     ap.add_argument("--op", choices=("decode", "append", "decode_append"), default="decode",
                     help="decode (default, the headline); append: paged KV-cache append; decode_append: "
                          "decode with one new token per row appended in the call")
@@ -431,7 +453,9 @@ def main() -> int:
             "data": "synthetic (seeded N(0,1) values, random paged layout; see pagedkv/configs.py)",
             "config": {**cfg.describe(), "schedule": res["schedule"], "splits": res["splits"],
                        "split_tokens": res["split_tokens"],
-                       "path": res["path"], "kv_sets": args.sets},
+                       "path": res["path"], "kv_sets": args.sets,
+                       **({"seqlen_q": args.seqlen_q, "causal": args.causal} if args.seqlen_q > 1 else {}),
+                       **({"window": list(args.window)} if tuple(args.window) != (-1, -1) else {})},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
             "hbm_frac_kv": round(res["kv_gbps"] / HBM_PEAK_GBPS, 4),

@@ -29,6 +29,11 @@ constexpr int64_t kMinTilesPerWorker = 8;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
+    int64_t M;        // query tokens per row
+    int64_t rows;     // query rows per KV head: M * group
+    int win_left;     // -1 = unbounded
+    int win_right;    // -1 = unbounded (0 with a causal mask and several query tokens)
+    bool multi_query; // several query tokens, a window or ALiBi: the masked MFMA policy
     int page_shift;
     int heads_per_wave;
     int head_groups;
@@ -85,11 +90,18 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (d->path != PKV_PATH_AUTO && d->path != PKV_PATH_VALU && d->path != PKV_PATH_MFMA) {
         return PKV_EINVAL;
     }
-    if (d->split_tokens < 0 || d->split_tokens % 16 != 0 || d->reserved != 0) {
+    if (d->split_tokens < 0 || d->split_tokens % 16 != 0 || d->reserved != 0 || d->reserved2 != 0) {
         return PKV_EINVAL;
     }
+    if (d->seqlen_q < 0 || (d->mask & ~(PKV_MASK_CAUSAL | PKV_MASK_WINDOW)) != 0 || d->alibi_batch_stride < 0) {
+        return PKV_EINVAL;
+    }
+    if ((d->mask & PKV_MASK_WINDOW) != 0 && (d->window_left < -1 || d->window_right < -1)) {
+        return PKV_EINVAL;
+    }
+    const int64_t M = std::max<int64_t>(1, d->seqlen_q);
     // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.
-    if (d->batch * d->num_heads > (int64_t{1} << 30) || d->num_pages > INT32_MAX ||
+    if (d->batch * d->num_heads * M > (int64_t{1} << 30) || d->num_pages > INT32_MAX ||
         d->block_table_stride > INT32_MAX) {
         return PKV_EUNSUPPORTED;
     }
@@ -99,13 +111,30 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     r.D = d->head_dim;
     r.P = d->page_size;
     r.group = r.H / r.Hk;
+    r.M = M;
+    r.rows = M * r.group;
+    // flash-attn 2.6.3: a causal mask is a right window of 0.  For one query
+    // token (at the last position) a right window changes nothing.
+    const bool window = (d->mask & PKV_MASK_WINDOW) != 0;
+    r.win_left = window ? d->window_left : -1;
+    r.win_right = window ? d->window_right : -1;
+    if ((d->mask & PKV_MASK_CAUSAL) != 0) {
+        r.win_right = 0;
+    }
+    if (M == 1) {
+        r.win_right = -1;
+    }
+    r.multi_query = M > 1 || r.win_left >= 0 || r.win_right >= 0 || d->alibi_slopes != nullptr;
     r.page_shift = ilog2(r.P);
     const int64_t row_cap = d->block_table_stride * r.P;
     const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
     r.max_pages = std::max<int64_t>(1, (max_seqlen + r.P - 1) / r.P);
     r.path = d->path == PKV_PATH_AUTO ? auto_path(r) : d->path;
+    if (r.multi_query && r.path != PKV_PATH_MFMA) {
+        return PKV_EUNSUPPORTED; // the VALU policy has one query token and no mask
+    }
     r.heads_per_wave = r.path == PKV_PATH_MFMA ? 16 : valu_heads_per_wave(r.group);
-    r.head_groups = static_cast<int>((r.group + r.heads_per_wave - 1) / r.heads_per_wave);
+    r.head_groups = static_cast<int>((r.rows + r.heads_per_wave - 1) / r.heads_per_wave);
     return PKV_OK;
 }
 
@@ -126,14 +155,18 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 // Streams of the tile-balanced schedule per row: (kv head, head group) pairs.
 int64_t streams_per_row(const Resolved& r) { return r.Hk * r.head_groups; }
 
-// Heads per partial slot of the tile-balanced schedule.
-int64_t part_heads(const Resolved& r) { return std::min<int64_t>(r.group, r.heads_per_wave); }
+// Query rows per partial slot of the tile-balanced schedule.
+int64_t part_heads(const Resolved& r) { return std::min<int64_t>(r.rows, r.heads_per_wave); }
 
 // Waves of the tile-balanced schedule: one workgroup per CU, fewer when the
-// upper bound of the call's tiles (every row at max_seqlen) would leave a wave
-// with under kMinTilesPerWorker tiles.
+// upper bound of the call's tiles (every row at max_seqlen, or at the span a
+// left window leaves) would leave a wave with under kMinTilesPerWorker tiles.
 int tile_workers(const Resolved& r, int64_t max_seqlen) {
-    const int64_t tiles = r.B * streams_per_row(r) * ((max_seqlen + 15) / 16);
+    int64_t span = max_seqlen;
+    if (r.win_left >= 0) {
+        span = std::min<int64_t>(span, r.M + r.win_left + 16);
+    }
+    const int64_t tiles = r.B * streams_per_row(r) * ((span + 15) / 16);
     const int64_t per_group = kMinTilesPerWorker * pkv::kTileWaves;
     const int64_t groups = std::clamp<int64_t>((tiles + per_group - 1) / per_group, 1, kComputeUnits);
     return static_cast<int>(groups * pkv::kTileWaves);
@@ -176,7 +209,7 @@ size_t partial_rows(const Resolved& r, const SplitPlan& plan) {
         return static_cast<size_t>(plan.splits + r.B * streams_per_row(r)) * static_cast<size_t>(part_heads(r));
     }
     if (plan.schedule == PKV_SCHED_PAGES || plan.schedule == PKV_SCHED_WINDOWS) {
-        return static_cast<size_t>(r.B * r.H) * static_cast<size_t>(plan.splits);
+        return static_cast<size_t>(r.B * r.H * r.M) * static_cast<size_t>(plan.splits);
     }
     return 0;
 }
@@ -265,6 +298,12 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.tile_workers = tiles ? plan.splits : 0;
     p.part_heads = static_cast<int32_t>(part_heads(r));
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;
+    p.q_len = static_cast<int32_t>(r.M);
+    p.rows = static_cast<int32_t>(r.rows);
+    p.win_left = r.win_left;
+    p.win_right = r.win_right;
+    p.alibi = desc->alibi_slopes;
+    p.alibi_stride = desc->alibi_batch_stride;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -287,7 +326,9 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.part_lse = p.part_lse;
         c.seqlens = cache_seqlens;
         c.out = p.out;
-        c.rows = static_cast<int32_t>(r.B * r.H);
+        c.rows = static_cast<int32_t>(r.B * r.M * r.H);
+        c.q_len = p.q_len;
+        c.win_left = p.win_left;
         c.num_heads = static_cast<int32_t>(r.H);
         c.splits = splits;
         c.split_tokens = plan.split_tokens;
@@ -539,7 +580,7 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
                 const int32_t* cache_seqlens, const int32_t* block_table, int64_t batch_size, int64_t seqlen_k,
                 int64_t seqlen_q, int64_t num_heads, int64_t num_heads_k, int64_t headdim, int64_t page_block_size,
                 int64_t num_blocks, int64_t causal) {
-    if (seqlen_q != 1 || causal != 0) {
+    if (seqlen_q < 1 || seqlen_q > INT32_MAX) {
         t_last_status = PKV_EUNSUPPORTED;
         return;
     }
@@ -558,6 +599,8 @@ void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_pa
     d.max_seqlen = seqlen_k > 0 ? seqlen_k : 0;
     d.dtype = PKV_DTYPE_BF16;
     d.path = PKV_PATH_AUTO;
+    d.seqlen_q = seqlen_q;
+    d.mask = causal != 0 ? PKV_MASK_CAUSAL : 0;
 
     std::lock_guard<std::mutex> lock(g_legacy_mutex);
     const size_t need = pkv_decode_workspace_size(&d, 0);

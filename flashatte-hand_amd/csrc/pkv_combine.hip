@@ -55,13 +55,22 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(CombinePara
     if (row >= p.rows) {
         return;
     }
-    const int seqlen = min(p.seqlens[row / p.num_heads], p.row_cap);
+    // Output row (b, i, h) of [B, M, H]; its partials sit at query row
+    // sr = (b * Hk + kv head) * M * group + i * group + g (= row when M = 1).
+    const int per_b = p.q_len * p.num_heads;
+    const int b = row / per_b;
+    const int i = (row - b * per_b) / p.num_heads;
+    const int h = row - b * per_b - i * p.num_heads;
+    const int kvh = h / p.group;
+    const int64_t sr = (static_cast<int64_t>(b) * (p.num_heads / p.group) + kvh) * p.q_len * p.group +
+                       i * p.group + (h - kvh * p.group);
+    const int seqlen = min(p.seqlens[b], p.row_cap);
     // Splits past the last token window are empty in split_tokens mode.
     const int n_loop = p.split_tokens > 0
                            ? (seqlen > 0 ? min(p.splits, (seqlen + p.split_tokens - 1) / p.split_tokens) : 0)
                            : p.splits;
-    const float* __restrict__ lse = p.part_lse + static_cast<int64_t>(row) * p.splits;
-    const float* __restrict__ o = p.part_o + static_cast<int64_t>(row) * p.splits * D + lane * E;
+    const float* __restrict__ lse = p.part_lse + sr * p.splits;
+    const float* __restrict__ o = p.part_o + sr * p.splits * D + lane * E;
 
     // First batch of partial rows, issued before the LSE loads are consumed.
     float x[kBatch][E];
@@ -149,17 +158,21 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     if (row >= p.rows) {
         return;
     }
-    const int b = row / p.num_heads;
-    const int h = row - b * p.num_heads;
+    // Output row (b, i, h) of [B, M, H] is query row r = i * group + g of
+    // stream (b, kv head, r / heads_per_wave).
+    const int per_b = p.q_len * p.num_heads;
+    const int b = row / per_b;
+    const int i = (row - b * per_b) / p.num_heads;
+    const int h = row - b * per_b - i * p.num_heads;
     const int kvh = h / p.group;
-    const int g = h - kvh * p.group;
-    const int hg = g / p.heads_per_wave;
-    const int hn = g - p.heads_per_wave * hg;
+    const int r = i * p.group + (h - kvh * p.group);
+    const int hg = r / p.heads_per_wave;
+    const int hn = r - p.heads_per_wave * hg;
     const int spr = (p.num_heads / p.group) * p.head_groups;
     const int u = kvh * p.head_groups + hg;
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
 
-    const int nb = row_tiles(p.seqlens, b, p.row_cap);
+    const int nb = row_tiles(p.seqlens, b, p.row_cap, p.q_len, p.win_left);
     if (nb == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -170,7 +183,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     int64_t before = 0;
     int64_t all = 0;
     for (int32_t bb = lane; bb < p.batch; bb += 64) {
-        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap));
+        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left));
         all += t;
         before += bb < b ? t : 0;
     }
@@ -216,7 +229,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     for (int e = 0; e < E; ++e) {
         acc[e] = 0.f;
     }
-    float wl = lane < parts ? fast_exp2(l0 - mx) : 0.f; // weight of part k0 + lane
+    // Weight of part lane; a part whose rows saw no visible key (masks) has
+    // lse = -inf and weighs 0, also when every part is empty (mx = -inf).
+    float wl = (lane < parts && l0 != kNegInf) ? fast_exp2(l0 - mx) : 0.f;
     float den = wl;
 #pragma unroll
     for (int v = 0; v < kBatch; ++v) {
@@ -231,8 +246,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     for (int k = kBatch; k < parts; k += kBatch) {
         if ((k & 63) == 0) {
             const int kl = k + lane;
-            // Every part has at least one token, so its LSE is finite.
-            wl = kl < parts ? fast_exp2(lse[kl * lse_stride] - mx) : 0.f;
+            const float lk = kl < parts ? lse[kl * lse_stride] : kNegInf;
+            wl = lk != kNegInf ? fast_exp2(lk - mx) : 0.f;
             den += wl;
         }
         float y[kBatch][E];

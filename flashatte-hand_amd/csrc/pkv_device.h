@@ -38,8 +38,17 @@ struct PartitionParams {
     int32_t num_items;    // splits * B * Hk * head_groups
     int32_t num_groups;   // workgroups in the grid
     int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
-    int32_t part_heads;   // heads per partial slot in the tile-balanced schedule
+    int32_t part_heads;   // rows per partial slot in the tile-balanced schedule
     float scale_log2;     // softmax_scale * log2(e)
+    // Query rows: each KV head serves rows = q_len * group query rows,
+    // r = i * group + g for query token i and head g of the group.  With
+    // q_len == 1 and no mask the kernels take the plain decode path.
+    int32_t q_len;        // M: query tokens per row (q, out [B, M, H, D])
+    int32_t rows;         // q_len * group
+    int32_t win_left;     // keys j >= pos - win_left; -1 = unbounded
+    int32_t win_right;    // keys j <= pos + win_right; -1 = unbounded (0 when causal)
+    const float* alibi;   // fp32 slopes at alibi[b * alibi_stride + h], or null
+    int64_t alibi_stride;
 };
 
 struct CombineParams {
@@ -60,7 +69,9 @@ struct CombineParams {
     int32_t batch;
     int32_t group;        // H / Hk
     int32_t head_groups;  // streams per (b, kv head)
-    int32_t heads_per_wave; // query heads per stream (16 MFMA, 1/2/4 VALU)
+    int32_t heads_per_wave; // query rows per stream (16 MFMA, 1/2/4 VALU)
+    int32_t q_len;        // as in PartitionParams; rows = B * q_len * H
+    int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
 };
 
 // Paged KV-cache append (pkv_append.hip): one 16-byte chunk of K and of V per
@@ -328,8 +339,9 @@ __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams&
 
 // ---------------------------------------------------------------- tile-balanced schedule
 //
-// A stream is the work of one (b, kv head, head group): the n_b = ceil(seqlen_b / 16)
-// tiles of 16 tokens of row b.  Streams are numbered r = b * spr + u with
+// A stream is the work of one (b, kv head, head group): the n_b tiles of 16
+// tokens of row b that its queries can see (tile_span: every tile of the row
+// unless a left window cuts the front).  Streams are numbered r = b * spr + u with
 // u = kv head * head_groups + head group (spr streams per row) and laid end to
 // end in that order as units_b = stream_units(n_b) balancing units each
 // (kHeaderTiles header units, then the tiles), so the call is one sequence of
@@ -345,8 +357,29 @@ __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams&
 // w(x) = floor(((x + 1) W - 1) / T), the worker owning unit x; tile t of
 // stream r is unit spr * C_b + u * units_b + kHeaderTiles + t.
 
-__device__ __forceinline__ int32_t row_tiles(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap) {
-    return (min(max(seqlens[b], 0), row_cap) + 15) >> 4;
+// Tiles a row's streams cover: from the tile of the first key any query of the
+// row can see to the row's last tile.  Without a left window that is every
+// tile of the row; with one, query 0 (at position L - q_len) sees keys from
+// L - q_len - win_left on, and no query sees anything earlier.
+struct TileSpan {
+    int32_t first; // first tile of the span
+    int32_t n;     // tiles in the span (0 for an empty row)
+};
+
+__device__ __forceinline__ TileSpan tile_span(int32_t sl, int32_t q_len, int32_t win_left) {
+    TileSpan t;
+    t.first = win_left >= 0 ? (min(max(sl - q_len - win_left, 0), sl) >> 4) : 0;
+    t.n = ((sl + 15) >> 4) - t.first;
+    return t;
+}
+
+__device__ __forceinline__ int32_t clamped_seqlen(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap) {
+    return min(max(seqlens[b], 0), row_cap);
+}
+
+__device__ __forceinline__ int32_t row_tiles(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap,
+                                             int32_t q_len, int32_t win_left) {
+    return tile_span(clamped_seqlen(seqlens, b, row_cap), q_len, win_left).n;
 }
 
 // Balancing units of a stream with n tiles: its tiles plus kHeaderTiles for
@@ -386,12 +419,12 @@ struct RowTiles {
 };
 
 __device__ __forceinline__ RowTiles locate_row(const int32_t* __restrict__ seqlens, int32_t batch, int32_t row_cap,
-                                               int64_t y, int32_t lane) {
+                                               int32_t q_len, int32_t win_left, int64_t y, int32_t lane) {
     int64_t carry = 0;
     for (int32_t base = 0; base < batch; base += 64) {
         const int32_t b = base + lane;
-        const int32_t sl = b < batch ? min(max(seqlens[b], 0), row_cap) : 0;
-        const int32_t n = (sl + 15) >> 4;
+        const int32_t sl = b < batch ? clamped_seqlen(seqlens, b, row_cap) : 0;
+        const int32_t n = tile_span(sl, q_len, win_left).n;
         const int32_t un = stream_units(n);
         int64_t incl = un;
 #pragma unroll
@@ -462,10 +495,10 @@ struct RowScan {
 };
 
 __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens, int32_t batch, int32_t row_cap,
-                                             int32_t lane) {
+                                             int32_t q_len, int32_t win_left, int32_t lane) {
     RowScan rs;
-    rs.sl0 = lane < batch ? min(max(seqlens[lane], 0), row_cap) : 0;
-    rs.n0 = (rs.sl0 + 15) >> 4;
+    rs.sl0 = lane < batch ? clamped_seqlen(seqlens, lane, row_cap) : 0;
+    rs.n0 = tile_span(rs.sl0, q_len, win_left).n;
     // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so 64 rows of
     // them fit 32 bits when row_cap <= 2^24.
     rs.fast = batch <= 64 && row_cap <= (1 << 24);
@@ -477,7 +510,7 @@ __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens
     rs.incl = 0;
     int64_t sum = stream_units(rs.n0);
     for (int32_t b = lane + 64; b < batch; b += 64) {
-        sum += stream_units(row_tiles(seqlens, b, row_cap));
+        sum += stream_units(row_tiles(seqlens, b, row_cap, q_len, win_left));
     }
     rs.rows_total = wave_sum_i64(sum);
     return rs;
@@ -485,7 +518,8 @@ __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens
 
 // Row holding stream-unit index y (0 <= y < rows_total).
 __device__ __forceinline__ RowTiles locate_unit_row(const RowScan& rs, const int32_t* __restrict__ seqlens,
-                                                    int32_t batch, int32_t row_cap, int64_t y, int32_t lane) {
+                                                    int32_t batch, int32_t row_cap, int32_t q_len, int32_t win_left,
+                                                    int64_t y, int32_t lane) {
     if (rs.fast) {
         const uint64_t hit = __ballot(lane < batch && rs.incl > static_cast<uint32_t>(y));
         const int32_t l = __builtin_ctzll(hit); // hit != 0 for y < rows_total
@@ -496,7 +530,7 @@ __device__ __forceinline__ RowTiles locate_unit_row(const RowScan& rs, const int
         r.before = static_cast<int64_t>(__builtin_amdgcn_readlane(rs.incl, l)) - stream_units(r.n);
         return r;
     }
-    return locate_row(seqlens, batch, row_cap, y, lane);
+    return locate_row(seqlens, batch, row_cap, q_len, win_left, y, lane);
 }
 
 // floor(a * b / c) for a, b >= 0, c > 0, a * b < 2^63; 32-bit when it fits.

@@ -158,14 +158,39 @@ constexpr float kLazyRescaleLog2 = 8.0f;
 
 // ---------------------------------------------------------------- MFMA math
 
-template <bool BF16, int D>
+// Query rows: a slice is rows r_first .. r_first + rows_here - 1 of one
+// (b, kv head), row r = i * group + g being query token i of head g of the
+// group.  With one query token (MQ false) row r is head r of the group and the
+// slice's output rows are consecutive.  With MQ, every lane also carries its
+// row's visible key range [lo, hi), position and ALiBi slope (flash-attn
+// 2.6.3 masks: query i of M at position pos = i + L - M sees keys
+// pos - win_left <= j <= pos + win_right, j < L; ALiBi adds -slope |pos - j|).
+
+// Output row of query row r of (b, kvh), as an index into [B, M, H] rows.
+__device__ __forceinline__ int64_t query_out_row(const PartitionParams& p, int b, int kvh, int r) {
+    const int i = r / p.group;
+    const int g = r - i * p.group;
+    return (static_cast<int64_t>(b) * p.q_len + i) * p.num_heads + kvh * p.group + g;
+}
+
+template <bool BF16, int D, bool MQ>
 struct MfmaMath {
     static constexpr int kHeads = 16;
     static constexpr int DT = D / 16;
+    static constexpr bool kMultiQuery = MQ;
 
-    // QK B operand: head n of the slice, dims 8(4kk + j) .. +7 (zero past the slice).
+    // QK B operand: row n of the slice, dims 8(4kk + j) .. +7 (zero past the slice).
+    // MQ: the lane's row (n = lane & 15) output index, query token, visible key
+    // range [lo, hi), position and ALiBi slope in log2 units.
     struct Q {
         uint4 op[D / 32];
+        int64_t row;
+        int32_t qi;
+        int32_t head;
+        int32_t lo;
+        int32_t hi;
+        int32_t pos;
+        float slope;
     };
     // O^T tiles (lane (n, j): head n, dims 16 dt + 4j .. +3), reference max, denominator.
     struct Acc {
@@ -174,16 +199,57 @@ struct MfmaMath {
         float l;
     };
 
-    __device__ static void load_q(const PartitionParams& p, int64_t bh_first, int heads_here, int lane, Q& q) {
+    __device__ static int64_t out_row(const PartitionParams& p, int b, int kvh, int r) {
+        if constexpr (MQ) {
+            return query_out_row(p, b, kvh, r);
+        } else {
+            return static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r;
+        }
+    }
+
+    __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int rows_here, int lane,
+                                  Q& q) {
         const int n = lane & 15;
         const int j = lane >> 4;
+        int64_t row;
+        if constexpr (MQ) {
+            const int r = r_first + min(n, rows_here - 1);
+            q.qi = r / p.group;
+            q.head = kvh * p.group + (r - q.qi * p.group);
+            row = (static_cast<int64_t>(b) * p.q_len + q.qi) * p.num_heads + q.head;
+            q.row = row;
+        } else {
+            row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
+        }
 #pragma unroll
         for (int kk = 0; kk < D / 32; ++kk) {
-            if (n < heads_here) {
-                q.op[kk] = *reinterpret_cast<const uint4*>(p.q + (bh_first + n) * D + 8 * (4 * kk + j));
+            if (n < rows_here) {
+                q.op[kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
             } else {
                 q.op[kk] = make_uint4(0u, 0u, 0u, 0u);
             }
+        }
+    }
+
+    // MQ: the lane's visible key range and ALiBi slope for a row of seqlen keys.
+    __device__ static void set_mask(const PartitionParams& p, int b, int seqlen, int rows_here, int lane, Q& q) {
+        if constexpr (MQ) {
+            const int n = lane & 15;
+            const int pos = seqlen - p.q_len + q.qi;
+            int lo = 0;
+            int hi = seqlen;
+            if (p.win_left >= 0) {
+                lo = static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0}));
+            }
+            if (p.win_right >= 0) {
+                hi = static_cast<int>(min(static_cast<int64_t>(pos) + p.win_right + 1, static_cast<int64_t>(seqlen)));
+            }
+            q.lo = n < rows_here ? lo : 0;
+            q.hi = n < rows_here ? hi : 0;
+            q.pos = pos;
+            q.slope = p.alibi != nullptr ? p.alibi[static_cast<int64_t>(b) * p.alibi_stride + q.head] *
+                                               1.4426950408889634f
+                                         : 0.f;
         }
     }
 
@@ -201,6 +267,7 @@ struct MfmaMath {
                                 float scale_log2) {
         const int n = lane & 15;
         const int j = lane >> 4;
+        (void)n;
         // S^T = K Q^T; K read back in the A-operand layout.
         uint4 ka[D / 32];
         const uint16_t* kr = lds + n * VTile<D>::kRow + 8 * j;
@@ -217,13 +284,21 @@ struct MfmaMath {
         float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            sc[i] = (t0 + 4 * j + i) < end ? s[i] * scale_log2 : kNegInf;
+            const int t = t0 + 4 * j + i;
+            if constexpr (MQ) {
+                const float x = s[i] * scale_log2 - q.slope * fabsf(static_cast<float>(q.pos - t));
+                sc[i] = (t < end && t >= q.lo && t < q.hi) ? x : kNegInf;
+            } else {
+                sc[i] = t < end ? s[i] * scale_log2 : kNegInf;
+            }
         }
         float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         tmax = max_halves32(max_rows16(tmax));
         if (__any(tmax > a.m + kLazyRescaleLog2)) {
             const float m_new = tmax > a.m + kLazyRescaleLog2 ? tmax : a.m;
-            const float alpha = fast_exp2(a.m - m_new); // 0 on the first tile (m = -inf), 1 if unchanged
+            // 0 on the first tile (m = -inf), 1 if unchanged.  With masks a row
+            // can still have no visible key (m stays -inf): keep it at 1 there.
+            const float alpha = (MQ && m_new == a.m) ? 1.f : fast_exp2(a.m - m_new);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 a.o[dt] *= alpha;
@@ -231,10 +306,13 @@ struct MfmaMath {
             a.l *= alpha;
             a.m = m_new;
         }
+        // MQ: a row that has seen no visible key yet has m = -inf and only
+        // masked scores; measure them from 0 so they give exactly 0.
+        const float mref = (MQ && a.m == kNegInf) ? 0.f : a.m;
         float pr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            pr[i] = fast_exp2(sc[i] - a.m);
+            pr[i] = fast_exp2(sc[i] - mref);
         }
         a.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
         uint2 pb;
@@ -264,16 +342,18 @@ struct MfmaMath {
     // l holds this lane's 4-token partial sums; total over the 4 lanes of head n.
     __device__ static void finish(Acc& a) { a.l = sum_halves32(sum_rows16(a.l)); }
 
-    // Output rows bh_first + h: O / l rounded to 16 bits (RNE).
-    __device__ static void write_final(const PartitionParams& p, int64_t bh_first, int heads_here, const Acc& a,
-                                       int lane) {
+    // Output rows of the slice (bh_first + n with one query token, the lane's
+    // row with MQ): O / l rounded to 16 bits (RNE).
+    __device__ static void write_final(const PartitionParams& p, const Q& q, int64_t bh_first, int heads_here,
+                                       const Acc& a, int lane) {
         const int n = lane & 15;
         const int j = lane >> 4;
         if (n >= heads_here) {
             return;
         }
         const float inv = a.l > 0.f ? 1.f / a.l : 0.f;
-        uint16_t* dst = p.out + (bh_first + n) * D + 4 * j;
+        const int64_t row = MQ ? q.row : bh_first + n;
+        uint16_t* dst = p.out + row * D + 4 * j;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             uint2 w;
@@ -359,6 +439,7 @@ template <bool BF16, int D, int NH>
 struct ValuMath {
     static constexpr int kHeads = NH;
     static constexpr int E = D / 64; // output dims per lane and head
+    static constexpr bool kMultiQuery = false; // one query token, no mask
 
     // Lane (t, c) = (lane & 15, lane >> 4): q of every head, dims 8(4i + c) .. +7.
     struct Q {
@@ -371,8 +452,14 @@ struct ValuMath {
         float l[NH];
     };
 
-    __device__ static void load_q(const PartitionParams& p, int64_t bh_first, int heads_here, int lane, Q& q) {
+    __device__ static int64_t out_row(const PartitionParams& p, int b, int kvh, int r) {
+        return static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r;
+    }
+
+    __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int heads_here, int lane,
+                                  Q& q) {
         const int c = lane >> 4;
+        const int64_t bh_first = out_row(p, b, kvh, r_first);
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
 #pragma unroll
@@ -383,6 +470,8 @@ struct ValuMath {
             }
         }
     }
+
+    __device__ static void set_mask(const PartitionParams&, int, int, int, int, Q&) {}
 
     __device__ static void init(Acc& a) {
 #pragma unroll
@@ -468,8 +557,8 @@ struct ValuMath {
         }
     }
 
-    __device__ static void write_final(const PartitionParams& p, int64_t bh_first, int heads_here, const Acc& a,
-                                       int lane) {
+    __device__ static void write_final(const PartitionParams& p, const Q&, int64_t bh_first, int heads_here,
+                                       const Acc& a, int lane) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             if (h < heads_here) {
@@ -654,9 +743,12 @@ void partition_split_kernel(PartitionParams p) {
     const int kvh = it.kvh;
     const int hg = it.hg;
 
-    const int g_first = hg * Math::kHeads;
-    const int heads_here = min(Math::kHeads, p.group - g_first);
-    const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
+    const int r_first = hg * Math::kHeads;
+    const int heads_here = min(Math::kHeads, p.rows - r_first);
+    const int64_t bh_first = Math::out_row(p, b, kvh, r_first);
+    // Partials are indexed by query row of (b, kv head): the output row index
+    // itself when there is one query token.
+    const int64_t sr_first = (static_cast<int64_t>(b) * p.num_heads_k + kvh) * p.rows + r_first;
 
     const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
 
@@ -664,7 +756,7 @@ void partition_split_kernel(PartitionParams p) {
     // cache_seqlens, so their loads are issued together with its load: the
     // item prologue costs two dependent round trips instead of three.
     typename Math::Q q;
-    Math::load_q(p, bh_first, heads_here, lane, q);
+    Math::load_q(p, b, kvh, r_first, heads_here, lane, q);
     const bool windowed = p.split_tokens > 0;
     int win_base = 0;
     int win = 0;
@@ -676,6 +768,7 @@ void partition_split_kernel(PartitionParams p) {
     }
 
     const int seqlen = min(p.seqlens[b], p.row_cap);
+    Math::set_mask(p, b, seqlen, heads_here, lane, q);
     const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
 
     if (range.begin >= range.end) {
@@ -683,11 +776,12 @@ void partition_split_kernel(PartitionParams p) {
         // With several, the combine derives each row's non-empty splits from
         // cache_seqlens and never reads this item's slot, so nothing is written.
         if (p.splits == 1) {
-            constexpr int CH = D / 8; // 16-byte output chunks per head
+            constexpr int CH = D / 8; // 16-byte output chunks per row
             for (int idx = lane; idx < heads_here * CH; idx += 64) {
                 const int g = idx / CH;
                 const int c = idx % CH;
-                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + c * 8) = make_uint4(0u, 0u, 0u, 0u);
+                *reinterpret_cast<uint4*>(p.out + Math::out_row(p, b, kvh, r_first + g) * D + c * 8) =
+                    make_uint4(0u, 0u, 0u, 0u);
             }
         }
         return;
@@ -701,9 +795,9 @@ void partition_split_kernel(PartitionParams p) {
     attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], range.begin, range.end, lane,
                                        kvh, acc);
     if (p.splits == 1) {
-        Math::write_final(p, bh_first, heads_here, acc, lane);
+        Math::write_final(p, q, bh_first, heads_here, acc, lane);
     } else {
-        Math::write_partial(p, bh_first * p.splits + split, p.splits, heads_here, acc, lane);
+        Math::write_partial(p, sr_first * p.splits + split, p.splits, heads_here, acc, lane);
     }
 }
 
@@ -723,14 +817,16 @@ void partition_item_group_kernel(PartitionParams p) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const Item it = decode_item(static_cast<int32_t>(blockIdx.x), p);
-    const int g_first = it.hg * Math::kHeads;
-    const int heads_here = min(Math::kHeads, p.group - g_first);
-    const int64_t bh_first = static_cast<int64_t>(it.b) * p.num_heads + it.kvh * p.group + g_first;
+    const int r_first = it.hg * Math::kHeads;
+    const int heads_here = min(Math::kHeads, p.rows - r_first);
+    const int64_t bh_first = Math::out_row(p, it.b, it.kvh, r_first);
+    const int64_t sr_first = (static_cast<int64_t>(it.b) * p.num_heads_k + it.kvh) * p.rows + r_first;
     const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(it.b) * p.bt_stride;
 
     typename Math::Q q;
-    Math::load_q(p, bh_first, heads_here, lane, q);
+    Math::load_q(p, it.b, it.kvh, r_first, heads_here, lane, q);
     const int seqlen = min(p.seqlens[it.b], p.row_cap);
+    Math::set_mask(p, it.b, seqlen, heads_here, lane, q);
     const TokenRange range = split_tokens_of(seqlen, p.page_shift, it.split, p.splits, p.split_tokens);
     if (range.begin >= range.end) {
         // As in partition_split_kernel: zeros for an empty row, nothing for an empty split.
@@ -739,7 +835,8 @@ void partition_item_group_kernel(PartitionParams p) {
             for (int idx = lane; idx < heads_here * CH; idx += 64) {
                 const int g = idx / CH;
                 const int c = idx % CH;
-                *reinterpret_cast<uint4*>(p.out + (bh_first + g) * D + c * 8) = make_uint4(0u, 0u, 0u, 0u);
+                *reinterpret_cast<uint4*>(p.out + Math::out_row(p, it.b, it.kvh, r_first + g) * D + c * 8) =
+                    make_uint4(0u, 0u, 0u, 0u);
             }
         }
         return;
@@ -771,9 +868,9 @@ void partition_item_group_kernel(PartitionParams p) {
         Math::merge(acc, other);
     }
     if (p.splits == 1) {
-        Math::write_final(p, bh_first, heads_here, acc, lane);
+        Math::write_final(p, q, bh_first, heads_here, acc, lane);
     } else {
-        Math::write_partial(p, bh_first * p.splits + it.split, p.splits, heads_here, acc, lane);
+        Math::write_partial(p, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane);
     }
 }
 
@@ -794,7 +891,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         return;
     }
     const int32_t spr = p.num_heads_k * p.head_groups;
-    const RowScan scan = scan_rows(p.seqlens, p.batch, p.row_cap, lane);
+    const RowScan scan = scan_rows(p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left, lane);
     const TilePlan plan = make_tile_plan(static_cast<int64_t>(spr) * uniform(scan.rows_total), p.tile_workers);
     if (w >= plan.workers) {
         return;
@@ -804,10 +901,12 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
     // Streams the tiles among this worker's units [x0, x_end), stream by
     // stream; partials go to slot w + r.
     auto run_share = [&](int64_t x0, int64_t x_end) {
-        const RowTiles rt = locate_unit_row(scan, p.seqlens, p.batch, p.row_cap, muldiv(x0, 1, spr), lane);
+        const RowTiles rt = locate_unit_row(scan, p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left,
+                                            muldiv(x0, 1, spr), lane);
         int b = uniform(rt.b);
         int seqlen = uniform(rt.seqlen);
         int nb = uniform(rt.n);
+        int first = tile_span(seqlen, p.q_len, p.win_left).first;
         int units = stream_units(nb);
         const int64_t row_first = static_cast<int64_t>(spr) * uniform(rt.before); // first unit of row b
         int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));
@@ -819,22 +918,23 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
             if (t_lo < t_hi) {
                 const int kvh = u / p.head_groups;
                 const int hg = u - kvh * p.head_groups;
-                const int g_first = hg * Math::kHeads;
-                const int heads_here = min(Math::kHeads, p.group - g_first);
-                const int64_t bh_first = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + g_first;
+                const int r_first = hg * Math::kHeads;
+                const int heads_here = min(Math::kHeads, p.rows - r_first);
+                const int64_t bh_first = Math::out_row(p, b, kvh, r_first);
                 const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-                const int begin = t_lo * 16;
-                const int end = min(t_hi * 16, seqlen);
+                const int begin = (first + t_lo) * 16;
+                const int end = min((first + t_hi) * 16, seqlen);
 
                 typename Math::Q q;
-                Math::load_q(p, bh_first, heads_here, lane, q);
+                Math::load_q(p, b, kvh, r_first, heads_here, lane, q);
+                Math::set_mask(p, b, seqlen, heads_here, lane, q);
                 const int win_base = begin >> p.page_shift;
                 const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
                 typename Math::Acc acc;
                 attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc);
                 if (t_lo == 0 && t_hi == nb) {
-                    Math::write_final(p, bh_first, heads_here, acc, lane);
+                    Math::write_final(p, q, bh_first, heads_here, acc, lane);
                 } else {
                     const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
                     Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane);
@@ -849,9 +949,11 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 u = 0;
                 do {
                     ++b;
-                    seqlen = uniform(min(max(p.seqlens[b], 0), p.row_cap));
+                    seqlen = uniform(clamped_seqlen(p.seqlens, b, p.row_cap));
                 } while (seqlen == 0 && b + 1 < p.batch);
-                nb = (seqlen + 15) >> 4;
+                const TileSpan span = tile_span(seqlen, p.q_len, p.win_left);
+                first = span.first;
+                nb = span.n;
                 units = stream_units(nb);
             }
         }
@@ -914,8 +1016,15 @@ static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, cons
 template <bool BF16, int D>
 static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wave, hipStream_t stream,
                            const LaunchEvents& ev) {
+    const bool multi_query = p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr;
     if (mfma) {
-        return launch_math<MfmaMath<BF16, D>, D>(p, stream, ev);
+        if (multi_query) {
+            return launch_math<MfmaMath<BF16, D, true>, D>(p, stream, ev);
+        }
+        return launch_math<MfmaMath<BF16, D, false>, D>(p, stream, ev);
+    }
+    if (multi_query) {
+        return hipErrorInvalidValue; // the VALU policy has one query token and no mask
     }
     switch (heads_per_wave) {
     case 1: return launch_math<ValuMath<BF16, D, 1>, D>(p, stream, ev);

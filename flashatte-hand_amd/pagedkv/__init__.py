@@ -3,9 +3,10 @@
 Two call surfaces over the C ABI of ``libpkv_decode.so``:
 
 * :func:`flash_attn_with_kvcache` — the call the reference's evaluator makes
-  (scripts/evaluate_flashattn_submission.py:232-247): ``q [B,1,H,D]``,
+  (scripts/evaluate_flashattn_submission.py:232-247): ``q [B,M,H,D]``,
   ``k_cache/v_cache [num_pages,P,Hk,D]``, ``cache_seqlens``, ``block_table``,
-  ``softmax_scale``, ``num_splits`` (0 = heuristic, 1 = single pass).
+  ``softmax_scale``, ``num_splits`` (0 = heuristic, 1 = single pass); q may hold
+  several query tokens ([B,M,H,D]) with causal / window / ALiBi masks.
 * :func:`run_kernel` — the reference's 15-argument torch binding
   (scripts/evaluate_flashattn_submission.py:46-78 -> best_flashattn_kvcache_decode.cu:1186).
 
@@ -30,6 +31,8 @@ from ._lib import (  # noqa: F401  (re-exported constants)
     PKV_ELAUNCH,
     PKV_ENOWORKSPACE,
     PKV_EUNSUPPORTED,
+    PKV_MASK_CAUSAL,
+    PKV_MASK_WINDOW,
     PKV_MAX_SPLITS,
     PKV_OK,
     PKV_PATH_AUTO,
@@ -90,6 +93,11 @@ def make_desc(
     workspace: int = 0,
     workspace_bytes: int = 0,
     prof_events: int = 0,
+    seqlen_q: int = 1,
+    causal: bool = False,
+    window_size=(-1, -1),
+    alibi_slopes: int = 0,
+    alibi_batch_stride: int = 0,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -107,6 +115,13 @@ def make_desc(
     d.workspace = workspace or None
     d.workspace_bytes = workspace_bytes
     d.prof_events = prof_events or None
+    d.seqlen_q = seqlen_q
+    window_size = tuple(window_size)
+    d.mask = (PKV_MASK_CAUSAL if causal else 0) | (PKV_MASK_WINDOW if window_size != (-1, -1) else 0)
+    d.window_left, d.window_right = window_size
+    d.reserved2 = 0
+    d.alibi_slopes = alibi_slopes or None
+    d.alibi_batch_stride = alibi_batch_stride
     return d
 
 
@@ -155,8 +170,16 @@ def decode(
     prof_events: int = 0,
     k_new=None,
     v_new=None,
+    causal: bool = False,
+    window_size=(-1, -1),
+    alibi_slopes=None,
 ):
-    """Run the decode operator on device tensors; returns ``out`` ([B,1,H,D]).
+    """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
+
+    ``q`` is ``[B, M, H, D]``: M > 1 query tokens per row (speculative-decode
+    verify) sit at the last M positions of each row; ``causal``,
+    ``window_size`` and ``alibi_slopes`` (fp32 ``[H]`` or ``[B, H]``) follow
+    flash-attn 2.6.3.
 
     With ``k_new`` / ``v_new`` ([B, seqlen_new, Hk, D]) the new tokens are first
     written into the caches at each row's ``cache_seqlens`` position and the
@@ -169,18 +192,25 @@ def decode(
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("block_table", block_table),
                     ("cache_seqlens", cache_seqlens)):
         _check_cuda(name, t)
-    if q.dim() != 4 or q.shape[1] != 1:
-        raise PkvError(PKV_EUNSUPPORTED, "q must be [B, 1, H, D] (seqlen_q = 1)")
+    if q.dim() != 4 or q.shape[1] < 1:
+        raise PkvError(PKV_EINVAL, "q must be [B, M, H, D]")
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise PkvError(PKV_EINVAL, "k_cache / v_cache must both be [num_pages, P, Hk, D]")
     if block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
         raise PkvError(PKV_EINVAL, "block_table and cache_seqlens must be int32")
     if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
         raise PkvError(PKV_EINVAL, "q, k_cache and v_cache must share a dtype")
-    B, _, H, D = q.shape
+    B, M, H, D = q.shape
     num_pages, P, Hk, Dk = k_cache.shape
     if Dk != D or block_table.dim() != 2 or block_table.shape[0] != B or cache_seqlens.numel() != B:
         raise PkvError(PKV_EINVAL, "inconsistent shapes")
+    alibi_ptr, alibi_stride = 0, 0
+    if alibi_slopes is not None:
+        _check_cuda("alibi_slopes", alibi_slopes)
+        if alibi_slopes.dtype != torch.float32 or alibi_slopes.shape not in ((H,), (B, H)):
+            raise PkvError(PKV_EINVAL, "alibi_slopes must be fp32 [H] or [B, H]")
+        alibi_ptr = alibi_slopes.data_ptr()
+        alibi_stride = H if alibi_slopes.dim() == 2 else 0
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -195,7 +225,8 @@ def decode(
     desc = make_desc(
         batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
         block_table_stride=block_table.shape[1], dtype=_dtype_code(q.dtype), max_seqlen=max_seqlen, path=path,
-        split_tokens=split_tokens, prof_events=prof_events,
+        split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
+        alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride,
     )
     lib = _lib.load()
     if seqlen_new:
@@ -328,28 +359,27 @@ def flash_attn_with_kvcache(
     num_splits=0,
     return_softmax_lse=False,
 ):
-    """Paged decode with the reference evaluator's call signature (eval:232-247).
+    """Paged attention with the reference evaluator's call signature (eval:232-247).
 
-    Supported: seqlen_q = 1, paged caches with ``block_table`` and
-    ``cache_seqlens`` (a tensor or one int for every row), and new tokens
-    ``k`` / ``v`` [B, seqlen_new, Hk, D], written into the caches in place
-    before the attention, which then covers ``cache_seqlens + seqlen_new``
-    tokens (flash-attn 2.6.3).  ``causal`` is accepted (it is a no-op for one
-    query token at the end of the cache).  Anything else raises
-    PkvError(PKV_EUNSUPPORTED).
+    Supported (flash-attn 2.6.3 semantics): q [B, M, H, D] with M query tokens
+    at the last M positions of each row; paged caches with ``block_table`` and
+    ``cache_seqlens`` (a tensor or one int for every row); new tokens ``k`` /
+    ``v`` [B, seqlen_new, Hk, D], written into the caches in place before the
+    attention, which then covers ``cache_seqlens + seqlen_new`` tokens;
+    ``causal`` (bottom-right aligned), ``window_size`` and ``alibi_slopes``.
+    Rotary embedding, ``cache_batch_idx``, ``cache_leftpad``, ``softcap`` and
+    ``return_softmax_lse`` raise PkvError(PKV_EUNSUPPORTED).
     """
     if rotary_cos is not None or rotary_sin is not None:
         raise PkvError(PKV_EUNSUPPORTED, "rotary embedding of the new K")
     if cache_batch_idx is not None or cache_leftpad is not None:
         raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
-    if tuple(window_size) != (-1, -1) or softcap or alibi_slopes is not None:
-        raise PkvError(PKV_EUNSUPPORTED, "sliding window / softcap / ALiBi")
+    if softcap:
+        raise PkvError(PKV_EUNSUPPORTED, "softcap")
     if return_softmax_lse:
         raise PkvError(PKV_EUNSUPPORTED, "return_softmax_lse")
     if block_table is None or cache_seqlens is None:
         raise PkvError(PKV_EUNSUPPORTED, "only the paged layout (block_table + cache_seqlens) is implemented")
-    if q.shape[1] != 1:
-        raise PkvError(PKV_EUNSUPPORTED, "seqlen_q > 1")
     if isinstance(cache_seqlens, int):
         torch = _torch()
         cache_seqlens = torch.full((q.shape[0],), cache_seqlens, dtype=torch.int32, device=q.device)
@@ -357,7 +387,9 @@ def flash_attn_with_kvcache(
         k = k.contiguous()
     if v is not None:
         v = v.contiguous()
-    return decode(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k, v_new=v)
+    return decode(q.contiguous(), k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k,
+                  v_new=v, causal=causal, window_size=window_size,
+                  alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous())
 
 
 def run_kernel(

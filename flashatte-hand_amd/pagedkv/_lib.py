@@ -30,6 +30,9 @@ PKV_SCHED_PAGES = 2
 PKV_SCHED_WINDOWS = 3
 PKV_SCHED_TILES = 4
 
+PKV_MASK_CAUSAL = 1
+PKV_MASK_WINDOW = 2
+
 PKV_MAX_SPLITS = 256
 
 # Every function the header declares, with its ctypes signature.
@@ -69,6 +72,13 @@ class PkvDecodeDesc(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("prof_events", ctypes.c_void_p),
+        ("seqlen_q", ctypes.c_int64),
+        ("mask", ctypes.c_int32),
+        ("window_left", ctypes.c_int32),
+        ("window_right", ctypes.c_int32),
+        ("reserved2", ctypes.c_int32),
+        ("alibi_slopes", ctypes.c_void_p),
+        ("alibi_batch_stride", ctypes.c_int64),
     ]
 
 

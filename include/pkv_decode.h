@@ -31,7 +31,7 @@ extern "C" {
  * every entry point here reports what happened instead. */
 #define PKV_OK 0
 #define PKV_EINVAL 1           /* null pointer, non-positive or inconsistent dims, misaligned pointer */
-#define PKV_EUNSUPPORTED 2     /* dtype / head_dim / page size / seqlen_q / causal not supported */
+#define PKV_EUNSUPPORTED 2     /* dtype / head_dim / page size / path not supported for this shape */
 #define PKV_ENOWORKSPACE 3     /* workspace missing or smaller than pkv_decode_workspace_size() */
 #define PKV_ELAUNCH 4          /* a HIP launch or runtime call failed */
 
@@ -48,6 +48,11 @@ extern "C" {
 #define PKV_SCHED_PAGES 2      /* each row's pages cut into num_splits near-equal ranges (the reference's) */
 #define PKV_SCHED_WINDOWS 3    /* each row cut into fixed windows of split_tokens tokens */
 #define PKV_SCHED_TILES 4      /* the call's 16-token tiles dealt evenly to a fixed set of waves */
+
+/* Masks (pkv_decode_desc.mask), flash-attn 2.6.3 semantics with key positions
+ * 0 .. L-1 (L = the row's length) and query i of M at position i + L - M. */
+#define PKV_MASK_CAUSAL 1      /* query i sees keys j <= i + L - M (bottom-right aligned) */
+#define PKV_MASK_WINDOW 2      /* window_left / window_right apply (each -1 = unbounded) */
 
 /* Largest split count a single call may use (the reference caps at 64,
  * best_flashattn_kvcache_decode.cu:15). */
@@ -74,11 +79,28 @@ typedef struct pkv_decode_desc {
                                    start, combine end, recorded by the kernels' own dispatch packets
                                    (profiling only; NULL in use).  Without a combine, [2] and [3]
                                    are recorded right after the partition. */
+    /* Several query tokens per row and masking (a zero-initialised tail = one
+     * query token, no mask).  With seqlen_q = M > 1, q and out are
+     * [B, M, H, D]; query i of row b sits at position i + L - M, L =
+     * cache_seqlens[b] (plus the appended tokens for pkv_decode_append). */
+    int64_t seqlen_q;           /* M; 0 or 1 = one query token */
+    int32_t mask;               /* PKV_MASK_* bits */
+    int32_t window_left;        /* PKV_MASK_WINDOW: keys j >= pos - window_left (-1 = unbounded) */
+    int32_t window_right;       /* PKV_MASK_WINDOW: keys j <= pos + window_right (-1 = unbounded);
+                                   PKV_MASK_CAUSAL forces 0 */
+    int32_t reserved2;          /* must be 0 */
+    const float* alibi_slopes;  /* optional fp32 [H] or [B, H]: score -= slope * |pos - j| */
+    int64_t alibi_batch_stride; /* 0 for [H] slopes, H for [B, H] */
 } pkv_decode_desc;
 
 /*
- * Paged-KV decode attention, seqlen_q = 1, non-causal:
+ * Paged-KV decode attention:
  *   out[b,h,:] = softmax(softmax_scale * q[b,h,:] . K[b,kvh,t,:]) V[b,kvh,t,:]  over t < cache_seqlens[b]
+ * With desc->seqlen_q = M > 1 (speculative-decode verify, chunked prefill
+ * over a paged cache), each of the M query tokens of a row attends over the
+ * keys its mask leaves (causal, sliding window, ALiBi bias; flash-attn 2.6.3
+ * semantics); a query with no visible key gets zeros.  M > 1, masks and
+ * ALiBi need the MFMA path (PKV_PATH_AUTO or PKV_PATH_MFMA).
  * Replaces the reference's `extern "C" void run_kernel(...)` launch entry
  * (submission-oj/best_flashattn_kvcache_decode.cu:1186-1201) with the
  * north-star argument order and an explicit stream.
@@ -167,11 +189,12 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, voi
 
 /*
  * flash_attn_with_kvcache(q, k_cache, v_cache, k=k_new, v=v_new,
- * cache_seqlens=, block_table=) for seqlen_q = 1: appends k_new / v_new as
- * pkv_append_kv does, then attends over the first
- * max(cache_seqlens[b], 0) + seqlen_new tokens of each row (flash-attn 2.6.3
+ * cache_seqlens=, block_table=): appends k_new / v_new as pkv_append_kv
+ * does, then attends over the first max(cache_seqlens[b], 0) + seqlen_new
+ * tokens of each row with the desc's query tokens and masks (flash-attn 2.6.3
  * semantics; the reference's evaluator passes k = v = None,
- * scripts/evaluate_flashattn_submission.py:236-237).  desc->max_seqlen, when
+ * scripts/evaluate_flashattn_submission.py:236-237).  With seqlen_q =
+ * seqlen_new and a causal mask this is the speculative-decode verify step.  desc->max_seqlen, when
  * set, bounds cache_seqlens before the append.  The workspace must hold
  * pkv_decode_append_workspace_size(desc, num_splits, seqlen_new) bytes (it
  * always holds the per-row lengths, so it is never NULL); prof_events, when
@@ -195,6 +218,9 @@ const char* pkv_strerror(int status);
  * scripts/evaluate_flashattn_submission.py:29-44): bf16 tensors,
  * softmax_scale = 1/sqrt(headdim), heuristic splits, null stream,
  * block_table row stride = num_blocks / batch_size, seqlen_k = max seqlen.
+ * The reference returns without launching when seqlen_q != 1 or causal != 0
+ * (best:1202-1211); here q / output are [B, seqlen_q, H, D] and causal masks
+ * bottom-right aligned, as flash-attn does.
  * Like the reference it keeps a grow-only workspace owned by the library
  * and is therefore not reentrant.  Its status is available from
  * pkv_last_status() instead of being dropped.

@@ -159,9 +159,7 @@ def test_auto_path_is_a_kernel_family():
 def test_run_kernel_rejects_unsupported_modes_without_launching():
     lib = _lib.load()
     p = ctypes.c_void_p(4096)
-    lib.run_kernel(p, p, p, p, p, p, 4, 128, 2, 32, 8, 128, 16, 64, 0)   # seqlen_q = 2
-    assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
-    lib.run_kernel(p, p, p, p, p, p, 4, 128, 1, 32, 8, 128, 16, 64, 1)   # causal
+    lib.run_kernel(p, p, p, p, p, p, 4, 128, 0, 32, 8, 128, 16, 64, 0)   # seqlen_q = 0
     assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
     lib.run_kernel(p, p, p, p, p, p, 4, 128, 1, 32, 8, 96, 16, 64, 0)    # head_dim 96
     assert lib.pkv_last_status() == pagedkv.PKV_EUNSUPPORTED
@@ -256,3 +254,66 @@ def test_decode_append_without_workspace_is_reported_before_the_cache_is_written
     d.workspace_bytes = lib.pkv_decode_append_workspace_size(ctypes.byref(d), 4, 1)
     assert lib.pkv_decode_append(p, p, p, p, p, p, p, 1, float("nan"), 4, p, ctypes.byref(d), None) == \
         pagedkv.PKV_EINVAL
+
+
+# ------------------------------------------------------------------ several query tokens, masks
+
+@pytest.mark.parametrize("field,value,status", [
+    ("seqlen_q", -1, pagedkv.PKV_EINVAL),
+    ("mask", 4, pagedkv.PKV_EINVAL),
+    ("reserved2", 1, pagedkv.PKV_EINVAL),
+    ("alibi_batch_stride", -1, pagedkv.PKV_EINVAL),
+])
+def test_invalid_query_and_mask_fields_are_rejected(field, value, status):
+    lib = _lib.load()
+    d = base_desc()
+    setattr(d, field, value)
+    p = ctypes.c_void_p(16)
+    assert lib.pkv_decode(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None) == status
+    assert pagedkv.workspace_size(d, 0) == 0
+
+
+def test_window_bounds_below_minus_one_are_rejected():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    for window in ((-2, 0), (3, -2)):
+        d = base_desc(window_size=window)
+        assert lib.pkv_decode(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+    # Without the window bit the bounds are not read.
+    d = base_desc()
+    d.window_left = -7
+    assert pagedkv.workspace_size(d, 0) > 0
+
+
+def test_several_query_tokens_or_masks_need_the_mfma_path():
+    for kw in (dict(seqlen_q=4), dict(window_size=(64, -1)), dict(alibi_slopes=4096)):
+        d = base_desc(path=pagedkv.PKV_PATH_VALU, **kw)
+        assert pagedkv.schedule_for(d, 0) == 0
+        assert pagedkv.path_for(base_desc(**kw)) == pagedkv.PKV_PATH_MFMA
+    # A causal mask on one query token changes nothing, so VALU may take it.
+    assert pagedkv.schedule_for(base_desc(path=pagedkv.PKV_PATH_VALU, causal=True), 0) == pagedkv.PKV_SCHED_TILES
+
+
+def test_workspace_counts_query_rows():
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for M in (1, 2, 4, 5):
+        d = base_desc(seqlen_q=M)   # B 32, H 32, Hk 8: M * 4 query rows per KV head
+        rows = 32 * 32 * M * 8
+        assert pagedkv.workspace_size(d, 8) == align(rows * 128 * 4) + align(rows * 4)
+        # Tiles: (workers + streams) slots of min(16, rows per KV head) rows; rows per KV head
+        # beyond 16 add streams.
+        w = pagedkv.num_splits_for(d, 0)
+        per_kv = 4 * M
+        streams = 32 * 8 * ((per_kv + 15) // 16)
+        slot_rows = (w + streams) * min(per_kv, 16)
+        assert pagedkv.workspace_size(d, 0) == align(slot_rows * 128 * 4) + align(slot_rows * 4)
+
+
+def test_left_window_shrinks_the_tile_schedule():
+    """A left window bounds every row's span to about M + window tokens, so small
+    windows get fewer waves (each still with at least 8 tiles)."""
+    full = pagedkv.num_splits_for(base_desc(max_seqlen=65536), 0)
+    small = pagedkv.num_splits_for(base_desc(max_seqlen=65536, window_size=(64, 0)), 0)
+    assert full == 1024
+    # 32 rows x 8 KV heads x ceil((1 + 64 + 16) / 16) = 6 tiles = 1536 tiles: 48 workgroups of 4 waves.
+    assert small == 192
