@@ -133,7 +133,9 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (r.multi_query && r.path != PKV_PATH_MFMA) {
         return PKV_EUNSUPPORTED; // the VALU policy has one query token and no mask
     }
-    r.heads_per_wave = r.path == PKV_PATH_MFMA ? 16 : valu_heads_per_wave(r.group);
+    // MFMA: one block of 16 query rows per wave, or two when a KV head has
+    // more than 16 (the K/V tile is then read once for 32 rows).
+    r.heads_per_wave = r.path == PKV_PATH_MFMA ? (r.rows > 16 ? 32 : 16) : valu_heads_per_wave(r.group);
     r.head_groups = static_cast<int>((r.rows + r.heads_per_wave - 1) / r.heads_per_wave);
     return PKV_OK;
 }

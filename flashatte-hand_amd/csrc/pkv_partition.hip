@@ -173,30 +173,39 @@ __device__ __forceinline__ int64_t query_out_row(const PartitionParams& p, int b
     return (static_cast<int64_t>(b) * p.q_len + i) * p.num_heads + kvh * p.group + g;
 }
 
-template <bool BF16, int D, bool MQ>
+// NB blocks of 16 query rows per wave share each staged K/V tile: the K
+// A operand and the V^T reads are loaded once and feed NB QK and NB PV MFMA
+// chains, so a (b, kv head) with up to 16 NB query rows reads its K/V once.
+template <bool BF16, int D, bool MQ, int NB>
 struct MfmaMath {
-    static constexpr int kHeads = 16;
+    static constexpr int kHeads = 16 * NB;
     static constexpr int DT = D / 16;
     static constexpr bool kMultiQuery = MQ;
 
-    // QK B operand: row n of the slice, dims 8(4kk + j) .. +7 (zero past the slice).
-    // MQ: the lane's row (n = lane & 15) output index, query token, visible key
-    // range [lo, hi), position and ALiBi slope in log2 units.
+    // QK B operands: row 16 nb + n of the slice (n = lane & 15), dims
+    // 8(4kk + j) .. +7 (zero past the slice).  MQ: per block, the lane's row
+    // output index, query token, visible key range [lo, hi), position and
+    // ALiBi slope in log2 units; and wave-uniform bounds of the tiles that
+    // every row sees whole (no mask needed there).
     struct Q {
-        uint4 op[D / 32];
-        int64_t row;
-        int32_t qi;
-        int32_t head;
-        int32_t lo;
-        int32_t hi;
-        int32_t pos;
-        float slope;
+        uint4 op[NB][D / 32];
+        int64_t row[NB];
+        int32_t qi[NB];
+        int32_t head[NB];
+        int32_t lo[NB];
+        int32_t hi[NB];
+        int32_t pos[NB];
+        float slope[NB];
+        int32_t all_lo; // max over the slice's rows of lo
+        int32_t all_hi; // min over the slice's rows of hi
+        bool alibi;
     };
-    // O^T tiles (lane (n, j): head n, dims 16 dt + 4j .. +3), reference max, denominator.
+    // Per block: O^T tiles (lane (n, j): row n, dims 16 dt + 4j .. +3),
+    // reference max, denominator.
     struct Acc {
-        f32x4 o[DT];
-        float m;
-        float l;
+        f32x4 o[NB][DT];
+        float m[NB];
+        float l[NB];
     };
 
     __device__ static int64_t out_row(const PartitionParams& p, int b, int kvh, int r) {
@@ -209,57 +218,81 @@ struct MfmaMath {
 
     __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int rows_here, int lane,
                                   Q& q) {
-        const int n = lane & 15;
         const int j = lane >> 4;
-        int64_t row;
-        if constexpr (MQ) {
-            const int r = r_first + min(n, rows_here - 1);
-            q.qi = r / p.group;
-            q.head = kvh * p.group + (r - q.qi * p.group);
-            row = (static_cast<int64_t>(b) * p.q_len + q.qi) * p.num_heads + q.head;
-            q.row = row;
-        } else {
-            row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
-        }
 #pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk) {
-            if (n < rows_here) {
-                q.op[kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
+        for (int nb = 0; nb < NB; ++nb) {
+            const int n = 16 * nb + (lane & 15);
+            int64_t row;
+            if constexpr (MQ) {
+                const int r = r_first + min(n, rows_here - 1);
+                q.qi[nb] = r / p.group;
+                q.head[nb] = kvh * p.group + (r - q.qi[nb] * p.group);
+                row = (static_cast<int64_t>(b) * p.q_len + q.qi[nb]) * p.num_heads + q.head[nb];
+                q.row[nb] = row;
             } else {
-                q.op[kk] = make_uint4(0u, 0u, 0u, 0u);
+                row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
+            }
+#pragma unroll
+            for (int kk = 0; kk < D / 32; ++kk) {
+                if (n < rows_here) {
+                    q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
+                } else {
+                    q.op[nb][kk] = make_uint4(0u, 0u, 0u, 0u);
+                }
             }
         }
     }
 
-    // MQ: the lane's visible key range and ALiBi slope for a row of seqlen keys.
+    // MQ: the lane's visible key ranges and ALiBi slopes for a row of seqlen keys.
     __device__ static void set_mask(const PartitionParams& p, int b, int seqlen, int rows_here, int lane, Q& q) {
         if constexpr (MQ) {
-            const int n = lane & 15;
-            const int pos = seqlen - p.q_len + q.qi;
-            int lo = 0;
-            int hi = seqlen;
-            if (p.win_left >= 0) {
-                lo = static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0}));
+            int all_lo = 0;
+            int all_hi = seqlen;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int n = 16 * nb + (lane & 15);
+                const int pos = seqlen - p.q_len + q.qi[nb];
+                int lo = 0;
+                int hi = seqlen;
+                if (p.win_left >= 0) {
+                    lo = static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0}));
+                }
+                if (p.win_right >= 0) {
+                    hi = static_cast<int>(
+                        min(static_cast<int64_t>(pos) + p.win_right + 1, static_cast<int64_t>(seqlen)));
+                }
+                q.lo[nb] = n < rows_here ? lo : 0;
+                q.hi[nb] = n < rows_here ? hi : 0;
+                q.pos[nb] = pos;
+                q.slope[nb] = p.alibi != nullptr
+                                  ? p.alibi[static_cast<int64_t>(b) * p.alibi_stride + q.head[nb]] * 1.4426950408889634f
+                                  : 0.f;
+                if (n < rows_here) {
+                    all_lo = max(all_lo, lo);
+                    all_hi = min(all_hi, hi);
+                }
             }
-            if (p.win_right >= 0) {
-                hi = static_cast<int>(min(static_cast<int64_t>(pos) + p.win_right + 1, static_cast<int64_t>(seqlen)));
+#pragma unroll
+            for (int d = 1; d < 16; d <<= 1) {
+                all_lo = max(all_lo, __shfl_xor(all_lo, d, 64));
+                all_hi = min(all_hi, __shfl_xor(all_hi, d, 64));
             }
-            q.lo = n < rows_here ? lo : 0;
-            q.hi = n < rows_here ? hi : 0;
-            q.pos = pos;
-            q.slope = p.alibi != nullptr ? p.alibi[static_cast<int64_t>(b) * p.alibi_stride + q.head] *
-                                               1.4426950408889634f
-                                         : 0.f;
+            q.all_lo = uniform(all_lo);
+            q.all_hi = uniform(all_hi);
+            q.alibi = p.alibi != nullptr;
         }
     }
 
     __device__ static void init(Acc& a) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            a.o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a.o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            a.m[nb] = kNegInf;
+            a.l[nb] = 0.f;
         }
-        a.m = kNegInf;
-        a.l = 0.f;
     }
 
     // One staged tile (tokens t0 .. t0 + 15, valid below end).
@@ -267,57 +300,86 @@ struct MfmaMath {
                                 float scale_log2) {
         const int n = lane & 15;
         const int j = lane >> 4;
-        (void)n;
-        // S^T = K Q^T; K read back in the A-operand layout.
+        // S^T = K Q^T; K read back in the A-operand layout, shared by the blocks.
         uint4 ka[D / 32];
         const uint16_t* kr = lds + n * VTile<D>::kRow + 8 * j;
 #pragma unroll
         for (int kk = 0; kk < D / 32; ++kk) {
             ka[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
         }
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        f32x4 s[NB];
 #pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk) {
-            s = mfma_qk<BF16>(ka[kk], q.op[kk], s);
-        }
-        // Lane holds head n, tokens 4j + i.
-        float sc[4];
+        for (int nb = 0; nb < NB; ++nb) {
+            s[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = t0 + 4 * j + i;
-            if constexpr (MQ) {
-                const float x = s[i] * scale_log2 - q.slope * fabsf(static_cast<float>(q.pos - t));
-                sc[i] = (t < end && t >= q.lo && t < q.hi) ? x : kNegInf;
-            } else {
-                sc[i] = t < end ? s[i] * scale_log2 : kNegInf;
+            for (int kk = 0; kk < D / 32; ++kk) {
+                s[nb] = mfma_qk<BF16>(ka[kk], q.op[nb][kk], s[nb]);
             }
         }
-        float tmax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        tmax = max_halves32(max_rows16(tmax));
-        if (__any(tmax > a.m + kLazyRescaleLog2)) {
-            const float m_new = tmax > a.m + kLazyRescaleLog2 ? tmax : a.m;
-            // 0 on the first tile (m = -inf), 1 if unchanged.  With masks a row
-            // can still have no visible key (m stays -inf): keep it at 1 there.
-            const float alpha = (MQ && m_new == a.m) ? 1.f : fast_exp2(a.m - m_new);
+        // Lane holds row 16 nb + n, tokens 4j + i.  MQ: tiles every row sees
+        // whole, without ALiBi, take the plain path (a wave-uniform test).
+        float sc[NB][4];
+        bool plain = true;
+        if constexpr (MQ) {
+            plain = !q.alibi && t0 >= q.all_lo && t0 + 16 <= q.all_hi && t0 + 16 <= end;
+        }
+        if (plain) {
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[dt] *= alpha;
+            for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    sc[nb][i] = (t0 + 4 * j + i) < end ? s[nb][i] * scale_log2 : kNegInf;
+                }
             }
-            a.l *= alpha;
-            a.m = m_new;
-        }
-        // MQ: a row that has seen no visible key yet has m = -inf and only
-        // masked scores; measure them from 0 so they give exactly 0.
-        const float mref = (MQ && a.m == kNegInf) ? 0.f : a.m;
-        float pr[4];
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pr[i] = fast_exp2(sc[i] - mref);
+            for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = t0 + 4 * j + i;
+                    const float x = s[nb][i] * scale_log2 - q.slope[nb] * fabsf(static_cast<float>(q.pos[nb] - t));
+                    sc[nb][i] = (t < end && t >= q.lo[nb] && t < q.hi[nb]) ? x : kNegInf;
+                }
+            }
         }
-        a.l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-        uint2 pb;
-        pb.x = pack2_hw<BF16>(pr[0], pr[1]);
-        pb.y = pack2_hw<BF16>(pr[2], pr[3]);
+        float tmax[NB];
+        bool raise = false;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            tmax[nb] = fmaxf(fmaxf(sc[nb][0], sc[nb][1]), fmaxf(sc[nb][2], sc[nb][3]));
+            tmax[nb] = max_halves32(max_rows16(tmax[nb]));
+            raise = raise || tmax[nb] > a.m[nb] + kLazyRescaleLog2;
+        }
+        if (__any(raise)) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const float m_new = tmax[nb] > a.m[nb] + kLazyRescaleLog2 ? tmax[nb] : a.m[nb];
+                // 0 on the first tile (m = -inf), 1 if unchanged.  With masks a
+                // row can still have no visible key (m stays -inf): keep it at 1.
+                const float alpha = (MQ && m_new == a.m[nb]) ? 1.f : fast_exp2(a.m[nb] - m_new);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    a.o[nb][dt] *= alpha;
+                }
+                a.l[nb] *= alpha;
+                a.m[nb] = m_new;
+            }
+        }
+        uint2 pb[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            // MQ: a row that has seen no visible key yet has m = -inf and only
+            // masked scores; measure them from 0 so they give exactly 0.
+            const float mref = (MQ && a.m[nb] == kNegInf) ? 0.f : a.m[nb];
+            float pr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pr[i] = fast_exp2(sc[nb][i] - mref);
+            }
+            a.l[nb] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+            pb[nb].x = pack2_hw<BF16>(pr[0], pr[1]);
+            pb[nb].y = pack2_hw<BF16>(pr[2], pr[3]);
+        }
 
         // O^T tile dt: A = V^T needs V[4j + i][16 dt + n] (i = 0..3) in lane (n, j).
         // ds_read_b64_tr_b16 hands lane i of each 16-lane row the elements
@@ -334,93 +396,122 @@ struct MfmaMath {
             av[dt] = __builtin_bit_cast(uint2, t);
         }
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            a.o[dt] = mfma_pv<BF16>(av[dt], pb, a.o[dt]);
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a.o[nb][dt] = mfma_pv<BF16>(av[dt], pb[nb], a.o[nb][dt]);
+            }
         }
     }
 
-    // l holds this lane's 4-token partial sums; total over the 4 lanes of head n.
-    __device__ static void finish(Acc& a) { a.l = sum_halves32(sum_rows16(a.l)); }
+    // l holds this lane's 4-token partial sums; total over the 4 lanes of row n.
+    __device__ static void finish(Acc& a) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            a.l[nb] = sum_halves32(sum_rows16(a.l[nb]));
+        }
+    }
 
-    // Output rows of the slice (bh_first + n with one query token, the lane's
-    // row with MQ): O / l rounded to 16 bits (RNE).
+    // Output rows of the slice (bh_first + 16 nb + n with one query token, the
+    // lane's rows with MQ): O / l rounded to 16 bits (RNE).
     __device__ static void write_final(const PartitionParams& p, const Q& q, int64_t bh_first, int heads_here,
                                        const Acc& a, int lane) {
-        const int n = lane & 15;
         const int j = lane >> 4;
-        if (n >= heads_here) {
-            return;
-        }
-        const float inv = a.l > 0.f ? 1.f / a.l : 0.f;
-        const int64_t row = MQ ? q.row : bh_first + n;
-        uint16_t* dst = p.out + row * D + 4 * j;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            uint2 w;
-            w.x = pack2<BF16>(a.o[dt][0] * inv, a.o[dt][1] * inv);
-            w.y = pack2<BF16>(a.o[dt][2] * inv, a.o[dt][3] * inv);
-            *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
+        for (int nb = 0; nb < NB; ++nb) {
+            const int n = 16 * nb + (lane & 15);
+            if (n < heads_here) {
+                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
+                int64_t row;
+                if constexpr (MQ) {
+                    row = q.row[nb];
+                } else {
+                    row = bh_first + n;
+                }
+                uint16_t* dst = p.out + row * D + 4 * j;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    uint2 w;
+                    w.x = pack2<BF16>(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv);
+                    w.y = pack2<BF16>(a.o[nb][dt][2] * inv, a.o[nb][dt][3] * inv);
+                    *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
+                }
+            }
         }
     }
 
-    // Partial of head h at index part_base + h * part_stride: O / l in fp32 and
-    // the log2-domain LSE m + log2(l).
+    // Partial of slice row h at index part_base + h * part_stride: O / l in
+    // fp32 and the log2-domain LSE m + log2(l).
     __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
                                          int heads_here, const Acc& a, int lane) {
-        const int n = lane & 15;
         const int j = lane >> 4;
-        if (n >= heads_here) {
-            return;
-        }
-        const int64_t pi = part_base + n * part_stride;
-        const float inv = a.l > 0.f ? 1.f / a.l : 0.f;
-        float* dst = p.part_o + pi * D + 4 * j;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            *reinterpret_cast<float4*>(dst + 16 * dt) =
-                make_float4(a.o[dt][0] * inv, a.o[dt][1] * inv, a.o[dt][2] * inv, a.o[dt][3] * inv);
-        }
-        if (j == 0) {
-            p.part_lse[pi] = a.l > 0.f ? a.m + fast_log2(a.l) : kNegInf;
+        for (int nb = 0; nb < NB; ++nb) {
+            const int n = 16 * nb + (lane & 15);
+            if (n < heads_here) {
+                const int64_t pi = part_base + n * part_stride;
+                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
+                float* dst = p.part_o + pi * D + 4 * j;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    *reinterpret_cast<float4*>(dst + 16 * dt) =
+                        make_float4(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv, a.o[nb][dt][2] * inv,
+                                    a.o[nb][dt][3] * inv);
+                }
+                if (j == 0) {
+                    p.part_lse[pi] = a.l[nb] > 0.f ? a.m[nb] + fast_log2(a.l[nb]) : kNegInf;
+                }
+            }
         }
     }
 
     // Online-softmax merge of another wave's finished accumulator (same lane layout).
     __device__ static void merge(Acc& a, const Acc& b) {
-        const float m = fmaxf(a.m, b.m);
-        const float sa = a.m == kNegInf ? 0.f : fast_exp2(a.m - m);
-        const float sb = b.m == kNegInf ? 0.f : fast_exp2(b.m - m);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            a.o[dt] = a.o[dt] * sa + b.o[dt] * sb;
+        for (int nb = 0; nb < NB; ++nb) {
+            const float m = fmaxf(a.m[nb], b.m[nb]);
+            const float sa = a.m[nb] == kNegInf ? 0.f : fast_exp2(a.m[nb] - m);
+            const float sb = b.m[nb] == kNegInf ? 0.f : fast_exp2(b.m[nb] - m);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a.o[nb][dt] = a.o[nb][dt] * sa + b.o[nb][dt] * sb;
+            }
+            a.l[nb] = a.l[nb] * sa + b.l[nb] * sb;
+            a.m[nb] = m;
         }
-        a.l = a.l * sa + b.l * sb;
-        a.m = m;
     }
 
     // Accumulator through LDS, one float per lane and field (conflict-free).
-    static constexpr int kAccFloats = 4 * DT + 2;
+    static constexpr int kAccFloats = NB * (4 * DT + 2);
     __device__ static void store_lds(const Acc& a, float* base, int lane) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        for (int nb = 0; nb < NB; ++nb) {
+            float* bb = base + nb * (4 * DT + 2) * 64;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                base[(4 * dt + i) * 64 + lane] = a.o[dt][i];
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bb[(4 * dt + i) * 64 + lane] = a.o[nb][dt][i];
+                }
             }
+            bb[4 * DT * 64 + lane] = a.m[nb];
+            bb[(4 * DT + 1) * 64 + lane] = a.l[nb];
         }
-        base[4 * DT * 64 + lane] = a.m;
-        base[(4 * DT + 1) * 64 + lane] = a.l;
     }
     __device__ static void load_lds(Acc& a, const float* base, int lane) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+        for (int nb = 0; nb < NB; ++nb) {
+            const float* bb = base + nb * (4 * DT + 2) * 64;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a.o[dt][i] = base[(4 * dt + i) * 64 + lane];
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a.o[nb][dt][i] = bb[(4 * dt + i) * 64 + lane];
+                }
             }
+            a.m[nb] = bb[4 * DT * 64 + lane];
+            a.l[nb] = bb[(4 * DT + 1) * 64 + lane];
         }
-        a.m = base[4 * DT * 64 + lane];
-        a.l = base[(4 * DT + 1) * 64 + lane];
     }
 };
 
@@ -810,9 +901,10 @@ template <typename Math, int D, bool WIDE, int DEPTH>
 __global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
 void partition_item_group_kernel(PartitionParams p) {
     constexpr int kWaves = kWavesPerGroup;
-    static_assert(Math::kAccFloats * 64 * sizeof(float) <= 2 * VTile<D>::kElems * sizeof(uint16_t),
-                  "accumulator must fit the wave's LDS tiles");
-    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][2 * VTile<D>::kElems];
+    // Each wave's LDS holds its K/V tiles, and afterwards its parked accumulator.
+    constexpr int kWaveElems = Math::kAccFloats * 64 * 2 > 2 * VTile<D>::kElems ? Math::kAccFloats * 64 * 2
+                                                                                : 2 * VTile<D>::kElems;
+    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][kWaveElems];
 
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -1018,10 +1110,17 @@ static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wa
                            const LaunchEvents& ev) {
     const bool multi_query = p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr;
     if (mfma) {
-        if (multi_query) {
-            return launch_math<MfmaMath<BF16, D, true>, D>(p, stream, ev);
+        // 16 or 32 query rows per wave (heads_per_wave).
+        if (heads_per_wave == 32) {
+            if (multi_query) {
+                return launch_math<MfmaMath<BF16, D, true, 2>, D>(p, stream, ev);
+            }
+            return launch_math<MfmaMath<BF16, D, false, 2>, D>(p, stream, ev);
         }
-        return launch_math<MfmaMath<BF16, D, false>, D>(p, stream, ev);
+        if (multi_query) {
+            return launch_math<MfmaMath<BF16, D, true, 1>, D>(p, stream, ev);
+        }
+        return launch_math<MfmaMath<BF16, D, false, 1>, D>(p, stream, ev);
     }
     if (multi_query) {
         return hipErrorInvalidValue; // the VALU policy has one query token and no mask

@@ -133,12 +133,15 @@ def test_tile_schedule_plan():
     small = base_desc(batch=1, num_heads=8, num_heads_k=2, max_seqlen=256, block_table_stride=4)
     tiles = 1 * 2 * 1 * (256 // 16)                          # B * Hk * head groups * tiles per row
     assert pagedkv.num_splits_for(small, 0) == -(-tiles // (8 * TILE_WAVES)) * TILE_WAVES
-    # workspace: (workers + streams) slots of min(16, group) heads, fp32 rows + LSEs
+    # workspace: (workers + streams) slots of min(heads per wave, group) heads, fp32 rows + LSEs;
+    # an MFMA wave takes 16 heads, or 32 when the group is larger than 16
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    for desc, group in ((d, 4), (base_desc(num_heads=64, num_heads_k=2), 32)):
+    for desc, group in ((d, 4), (base_desc(num_heads=64, num_heads_k=2), 32),
+                        (base_desc(num_heads=96, num_heads_k=2), 48)):
         workers = pagedkv.num_splits_for(desc, 0)
-        streams = 32 * desc.num_heads_k * -(-group // 16)
-        rows = (workers + streams) * min(16, group)
+        per_wave = 32 if group > 16 else 16
+        streams = 32 * desc.num_heads_k * -(-group // per_wave)
+        rows = (workers + streams) * min(per_wave, group)
         assert pagedkv.workspace_size(desc, 0) == align(rows * 128 * 4) + align(rows * 4)
     # an explicit window or forced splits leave the tile schedule
     assert pagedkv.schedule_for(base_desc(split_tokens=512), 0) == pagedkv.PKV_SCHED_WINDOWS
@@ -296,16 +299,17 @@ def test_several_query_tokens_or_masks_need_the_mfma_path():
 
 def test_workspace_counts_query_rows():
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    for M in (1, 2, 4, 5):
+    for M in (1, 2, 4, 5, 8, 9):
         d = base_desc(seqlen_q=M)   # B 32, H 32, Hk 8: M * 4 query rows per KV head
         rows = 32 * 32 * M * 8
         assert pagedkv.workspace_size(d, 8) == align(rows * 128 * 4) + align(rows * 4)
-        # Tiles: (workers + streams) slots of min(16, rows per KV head) rows; rows per KV head
-        # beyond 16 add streams.
+        # Tiles: (workers + streams) slots of min(rows per wave, rows per KV head) rows; a wave
+        # takes 16 query rows, or 32 when a KV head has more than 16.
         w = pagedkv.num_splits_for(d, 0)
         per_kv = 4 * M
-        streams = 32 * 8 * ((per_kv + 15) // 16)
-        slot_rows = (w + streams) * min(per_kv, 16)
+        per_wave = 32 if per_kv > 16 else 16
+        streams = 32 * 8 * ((per_kv + per_wave - 1) // per_wave)
+        slot_rows = (w + streams) * min(per_kv, per_wave)
         assert pagedkv.workspace_size(d, 0) == align(slot_rows * 128 * 4) + align(slot_rows * 4)
 
 
