@@ -1,1152 +1,22 @@
-// pkv_partition.hip — partition kernels for paged-KV GQA decode on gfx950.
-//
-// One wave64 works on one head slice (one kv head and up to Math::kHeads of its
-// query heads) over a token range, in tiles of 16 tokens.  Per tile:
-//
-//   load   K and V rows in row layout (D/8 lanes per token, whole 128-byte
-//          lines, nontemporal 16-byte loads), page ids from a register window;
-//   stage  the rows into the wave's LDS tiles, then issue the next tile's
-//          loads into the freed registers (one tile in flight during compute);
-//   math   QK, online softmax (fp32, log2 domain, lazy rescale) and PV on the
-//          staged tile, by one of two policies:
-//     MfmaMath  16 heads per wave (zero-padded).  S^T[16 tok x 16 heads] =
-//               K Q^T with v_mfma_f32_16x16x32_{bf16,f16} (A = K from LDS,
-//               lane (n, j): token n, dims 8(4kk + j) .. +7; B = Q^T in VGPRs),
-//               then O^T[D x 16 heads] += V^T P^T with
-//               v_mfma_f32_16x16x16{bf16_1k,f16}, V^T from the LDS tile through
-//               ds_read_b64_tr_b16 and P^T packed to 16 bits in place;
-//     ValuMath  1, 2 or 4 heads per wave.  Lane (t, c) takes token t and a
-//               quarter of the dims: v_dot2 products, a cross-row sum, DPP row
-//               max/sum; PV with fp32 FMAs, each lane owning D/64 dims of
-//               every head and the probabilities broadcast with readlane.
-// The per-wave LDS tiles are private to the wave and LDS operations of a wave
-// complete in order, so no barrier is needed.
-//
-// Reference semantics followed: submission-oj/best_flashattn_kvcache_decode.cu
-// 595-954 (partition, page ranges 664-671, empty split 680-697, exp2 online
-// update 782-833, lse2 845-864); the MMA-QK idea of packing the GQA heads into
-// the M/N dimension is the reference's flashattn_kvcache_decode_mma_v2.cu:685-1001,
-// re-tiled here for 64-lane MFMA with PV also on MFMA.
-#include "pkv_device.h"
+// pkv_partition.hip — head_dim dispatch of the partition kernels (their
+// templates are in pkv_partition_impl.h, instantiated by pkv_part_d*.hip).
 #include "pkv_launch.h"
 
 namespace pkv {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_qk(const uint4& a, const uint4& b, f32x4 c) {
-    if constexpr (BF16) {
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                       0, 0, 0);
-    } else {
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                      0, 0, 0);
-    }
-}
-
-template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_pv(const uint2& a, const uint2& b, f32x4 c) {
-    if constexpr (BF16) {
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
-                                                         0, 0, 0);
-    } else {
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0,
-                                                     0, 0);
-    }
-}
-
-template <int D>
-struct TileRegs {
-    uint4 k[D / 32];
-    uint4 v[D / 32];
-};
-
-// Issue the K and V loads of the 16-token tile starting at t0 in row layout:
-// the L = D/8 lanes of a row read one token's D contiguous 16-bit values of
-// this KV head (whole 128-byte lines), so one instruction covers R = 64/L
-// tokens and a tile takes D/32 instructions per tensor.  (Reading the MFMA
-// operand layout straight from HBM — 16 tokens x 64 bytes per instruction —
-// streams measurably slower, so K is re-laid out through LDS instead.)
-// WIDE: P >= 16, so the tile lies inside one page whose id is wave-uniform and
-// is read from the page window with readlane; otherwise each lane fetches its
-// own token's page id from the window with ds_bpermute.  Neither waits on a
-// global load, so earlier tiles' loads stay in flight.  When `real` is false
-// (a prefetch past the end of the range) every lane loads the same 16 bytes at
-// the start of the caches instead: the loop then issues the same number of
-// loads on every path, which keeps the compiler's wait counts exact.
-template <int D, bool WIDE>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams& p, int win, int win_base, int t0,
-                                          int end, bool real, int lane, int kvh) {
-    constexpr int L = D / 8;
-    constexpr int R = 64 / L;
-    constexpr int NI = D / 32;
-    const int rl = lane / L;
-    const int pmask = (1 << p.page_shift) - 1;
-    const uint32_t col = static_cast<uint32_t>(kvh * D + 8 * (lane % L)) * 2u; // bytes within a token row
-    const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * 2u;            // bytes per token
-    if constexpr (WIDE) {
-        // Wave-uniform page base (SGPRs) + 32-bit lane offsets: saddr-form loads.
-        const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
-        const int phys = __builtin_amdgcn_readlane(win, idx);
-        const int64_t base =
-            real ? (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(t0 & pmask) * p.token_stride) * 2
-                 : 0;
-        const char* kb = reinterpret_cast<const char*>(p.k) + base;
-        const char* vb = reinterpret_cast<const char*>(p.v) + base;
-        const int lim = real ? end - 1 - t0 : 0; // clamp: never touch unowned slots
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const uint32_t off = real ? static_cast<uint32_t>(min(R * i + rl, lim)) * ts2 + col : 0u;
-            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(kb + off));
-            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(vb + off));
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int t = min(t0 + R * i + rl, end - 1);
-            const int phys = __shfl(win, real ? (t >> p.page_shift) - win_base : 0, 64);
-            const int64_t off =
-                real ? static_cast<int64_t>(phys) * p.page_stride * 2 + static_cast<int64_t>(t & pmask) * ts2 + col
-                     : 0;
-            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.k) + off));
-            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.v) + off));
-        }
-    }
-}
-
-// LDS tiles of one wave: 16 token rows of K and of V, each row padded by 32
-// bytes (row stride 2D + 32 bytes).  Measured with SQ_LDS_BANK_CONFLICT on
-// gfx950: with 16-byte padding the V transpose reads spent half their cycles
-// in bank conflicts (a quarter of the kernel's LDS cycles); with 32 bytes the
-// kernel has none, and the row writes are conflict-free with any padding.
-// Every address is a per-lane base plus an immediate offset.
-template <int D>
-struct VTile {
-    static constexpr int kRow = D + 16; // row stride in 16-bit elements
-    static constexpr int kElems = 16 * kRow;
-};
-
-// Part 1a of a tile: stage the K and V rows in the wave's LDS tiles.  After
-// this the tile's registers are free for the next prefetch.
-template <int D>
-__device__ __forceinline__ void stage_tile(const TileRegs<D>& r, uint16_t* lds, int lane) {
-    constexpr int L = D / 8;
-    constexpr int R = 64 / L;
-    constexpr int NI = D / 32;
-    uint16_t* kt = lds;
-    uint16_t* vt = lds + VTile<D>::kElems;
-    const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
-        *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
-    }
-}
-
-// Rescale threshold of the running max (log2 units): probabilities are taken
-// relative to a reference max m that is only raised when a tile's max exceeds
-// it by more than this, so p <= 2^8 (exact in fp16/bf16 range) and the
-// accumulator rescale runs only a handful of times per item.  The result is
-// the same softmax: numerator and denominator share the reference.
-constexpr float kLazyRescaleLog2 = 8.0f;
-
-// ---------------------------------------------------------------- MFMA math
-
-// Query rows: a slice is rows r_first .. r_first + rows_here - 1 of one
-// (b, kv head), row r = i * group + g being query token i of head g of the
-// group.  With one query token (MQ false) row r is head r of the group and the
-// slice's output rows are consecutive.  With MQ, every lane also carries its
-// row's visible key range [lo, hi), position and ALiBi slope (flash-attn
-// 2.6.3 masks: query i of M at position pos = i + L - M sees keys
-// pos - win_left <= j <= pos + win_right, j < L; ALiBi adds -slope |pos - j|).
-
-// Output row of query row r of (b, kvh), as an index into [B, M, H] rows.
-__device__ __forceinline__ int64_t query_out_row(const PartitionParams& p, int b, int kvh, int r) {
-    const int i = r / p.group;
-    const int g = r - i * p.group;
-    return (static_cast<int64_t>(b) * p.q_len + i) * p.num_heads + kvh * p.group + g;
-}
-
-// NB blocks of 16 query rows per wave share each staged K/V tile: the K
-// A operand and the V^T reads are loaded once and feed NB QK and NB PV MFMA
-// chains, so a (b, kv head) with up to 16 NB query rows reads its K/V once.
-template <bool BF16, int D, bool MQ, int NB>
-struct MfmaMath {
-    static constexpr int kHeads = 16 * NB;
-    static constexpr int DT = D / 16;
-    static constexpr bool kMultiQuery = MQ;
-
-    // QK B operands: row 16 nb + n of the slice (n = lane & 15), dims
-    // 8(4kk + j) .. +7 (zero past the slice).  MQ: per block, the lane's row
-    // output index, query token, visible key range [lo, hi), position and
-    // ALiBi slope in log2 units; and wave-uniform bounds of the tiles that
-    // every row sees whole (no mask needed there).
-    struct Q {
-        uint4 op[NB][D / 32];
-        int64_t row[NB];
-        int32_t qi[NB];
-        int32_t head[NB];
-        int32_t lo[NB];
-        int32_t hi[NB];
-        int32_t pos[NB];
-        float slope[NB];
-        int32_t all_lo; // max over the slice's rows of lo
-        int32_t all_hi; // min over the slice's rows of hi
-        bool alibi;
-    };
-    // Per block: O^T tiles (lane (n, j): row n, dims 16 dt + 4j .. +3),
-    // reference max, denominator.
-    struct Acc {
-        f32x4 o[NB][DT];
-        float m[NB];
-        float l[NB];
-    };
-
-    __device__ static int64_t out_row(const PartitionParams& p, int b, int kvh, int r) {
-        if constexpr (MQ) {
-            return query_out_row(p, b, kvh, r);
-        } else {
-            return static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r;
-        }
-    }
-
-    __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int rows_here, int lane,
-                                  Q& q) {
-        const int j = lane >> 4;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int n = 16 * nb + (lane & 15);
-            int64_t row;
-            if constexpr (MQ) {
-                const int r = r_first + min(n, rows_here - 1);
-                q.qi[nb] = r / p.group;
-                q.head[nb] = kvh * p.group + (r - q.qi[nb] * p.group);
-                row = (static_cast<int64_t>(b) * p.q_len + q.qi[nb]) * p.num_heads + q.head[nb];
-                q.row[nb] = row;
-            } else {
-                row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
-            }
-#pragma unroll
-            for (int kk = 0; kk < D / 32; ++kk) {
-                if (n < rows_here) {
-                    q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
-                } else {
-                    q.op[nb][kk] = make_uint4(0u, 0u, 0u, 0u);
-                }
-            }
-        }
-    }
-
-    // MQ: the lane's visible key ranges and ALiBi slopes for a row of seqlen keys.
-    __device__ static void set_mask(const PartitionParams& p, int b, int seqlen, int rows_here, int lane, Q& q) {
-        if constexpr (MQ) {
-            int all_lo = 0;
-            int all_hi = seqlen;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const int n = 16 * nb + (lane & 15);
-                const int pos = seqlen - p.q_len + q.qi[nb];
-                int lo = 0;
-                int hi = seqlen;
-                if (p.win_left >= 0) {
-                    lo = static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0}));
-                }
-                if (p.win_right >= 0) {
-                    hi = static_cast<int>(
-                        min(static_cast<int64_t>(pos) + p.win_right + 1, static_cast<int64_t>(seqlen)));
-                }
-                q.lo[nb] = n < rows_here ? lo : 0;
-                q.hi[nb] = n < rows_here ? hi : 0;
-                q.pos[nb] = pos;
-                q.slope[nb] = p.alibi != nullptr
-                                  ? p.alibi[static_cast<int64_t>(b) * p.alibi_stride + q.head[nb]] * 1.4426950408889634f
-                                  : 0.f;
-                if (n < rows_here) {
-                    all_lo = max(all_lo, lo);
-                    all_hi = min(all_hi, hi);
-                }
-            }
-#pragma unroll
-            for (int d = 1; d < 16; d <<= 1) {
-                all_lo = max(all_lo, __shfl_xor(all_lo, d, 64));
-                all_hi = min(all_hi, __shfl_xor(all_hi, d, 64));
-            }
-            q.all_lo = uniform(all_lo);
-            q.all_hi = uniform(all_hi);
-            q.alibi = p.alibi != nullptr;
-        }
-    }
-
-    __device__ static void init(Acc& a) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-            a.m[nb] = kNegInf;
-            a.l[nb] = 0.f;
-        }
-    }
-
-    // One staged tile (tokens t0 .. t0 + 15, valid below end).
-    __device__ static void tile(const Q& q, Acc& a, const uint16_t* lds, int t0, int end, int lane,
-                                float scale_log2) {
-        const int n = lane & 15;
-        const int j = lane >> 4;
-        // S^T = K Q^T; K read back in the A-operand layout, shared by the blocks.
-        uint4 ka[D / 32];
-        const uint16_t* kr = lds + n * VTile<D>::kRow + 8 * j;
-#pragma unroll
-        for (int kk = 0; kk < D / 32; ++kk) {
-            ka[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
-        }
-        f32x4 s[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            s[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < D / 32; ++kk) {
-                s[nb] = mfma_qk<BF16>(ka[kk], q.op[nb][kk], s[nb]);
-            }
-        }
-        // Lane holds row 16 nb + n, tokens 4j + i.  MQ: tiles every row sees
-        // whole, without ALiBi, take the plain path (a wave-uniform test).
-        float sc[NB][4];
-        bool plain = true;
-        if constexpr (MQ) {
-            plain = !q.alibi && t0 >= q.all_lo && t0 + 16 <= q.all_hi && t0 + 16 <= end;
-        }
-        if (plain) {
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    sc[nb][i] = (t0 + 4 * j + i) < end ? s[nb][i] * scale_log2 : kNegInf;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int t = t0 + 4 * j + i;
-                    const float x = s[nb][i] * scale_log2 - q.slope[nb] * fabsf(static_cast<float>(q.pos[nb] - t));
-                    sc[nb][i] = (t < end && t >= q.lo[nb] && t < q.hi[nb]) ? x : kNegInf;
-                }
-            }
-        }
-        float tmax[NB];
-        bool raise = false;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            tmax[nb] = fmaxf(fmaxf(sc[nb][0], sc[nb][1]), fmaxf(sc[nb][2], sc[nb][3]));
-            tmax[nb] = max_halves32(max_rows16(tmax[nb]));
-            raise = raise || tmax[nb] > a.m[nb] + kLazyRescaleLog2;
-        }
-        if (__any(raise)) {
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const float m_new = tmax[nb] > a.m[nb] + kLazyRescaleLog2 ? tmax[nb] : a.m[nb];
-                // 0 on the first tile (m = -inf), 1 if unchanged.  With masks a
-                // row can still have no visible key (m stays -inf): keep it at 1.
-                const float alpha = (MQ && m_new == a.m[nb]) ? 1.f : fast_exp2(a.m[nb] - m_new);
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    a.o[nb][dt] *= alpha;
-                }
-                a.l[nb] *= alpha;
-                a.m[nb] = m_new;
-            }
-        }
-        uint2 pb[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            // MQ: a row that has seen no visible key yet has m = -inf and only
-            // masked scores; measure them from 0 so they give exactly 0.
-            const float mref = (MQ && a.m[nb] == kNegInf) ? 0.f : a.m[nb];
-            float pr[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pr[i] = fast_exp2(sc[nb][i] - mref);
-            }
-            a.l[nb] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-            pb[nb].x = pack2_hw<BF16>(pr[0], pr[1]);
-            pb[nb].y = pack2_hw<BF16>(pr[2], pr[3]);
-        }
-
-        // O^T tile dt: A = V^T needs V[4j + i][16 dt + n] (i = 0..3) in lane (n, j).
-        // ds_read_b64_tr_b16 hands lane i of each 16-lane row the elements
-        // M[i / 4 + 4e][i % 4] (e = 0..3) of the 4-element chunks M[r] its row's
-        // lanes address, so lane (n, j) addresses V[4j + n / 4][16 dt + 4 (n % 4)].
-        typedef short s16x4_t __attribute__((ext_vector_type(4)));
-        typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
-        const uint16_t* rd = lds + VTile<D>::kElems + (4 * j + (n >> 2)) * VTile<D>::kRow + 4 * (n & 3);
-        uint2 av[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const s16x4_t t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)((__attribute__((address_space(3))) uint16_t*)(rd + 16 * dt)));
-            av[dt] = __builtin_bit_cast(uint2, t);
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = mfma_pv<BF16>(av[dt], pb[nb], a.o[nb][dt]);
-            }
-        }
-    }
-
-    // l holds this lane's 4-token partial sums; total over the 4 lanes of row n.
-    __device__ static void finish(Acc& a) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            a.l[nb] = sum_halves32(sum_rows16(a.l[nb]));
-        }
-    }
-
-    // Output rows of the slice (bh_first + 16 nb + n with one query token, the
-    // lane's rows with MQ): O / l rounded to 16 bits (RNE).
-    __device__ static void write_final(const PartitionParams& p, const Q& q, int64_t bh_first, int heads_here,
-                                       const Acc& a, int lane) {
-        const int j = lane >> 4;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int n = 16 * nb + (lane & 15);
-            if (n < heads_here) {
-                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
-                int64_t row;
-                if constexpr (MQ) {
-                    row = q.row[nb];
-                } else {
-                    row = bh_first + n;
-                }
-                uint16_t* dst = p.out + row * D + 4 * j;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    uint2 w;
-                    w.x = pack2<BF16>(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv);
-                    w.y = pack2<BF16>(a.o[nb][dt][2] * inv, a.o[nb][dt][3] * inv);
-                    *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
-                }
-            }
-        }
-    }
-
-    // Partial of slice row h at index part_base + h * part_stride: O / l in
-    // fp32 and the log2-domain LSE m + log2(l).
-    __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
-                                         int heads_here, const Acc& a, int lane) {
-        const int j = lane >> 4;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int n = 16 * nb + (lane & 15);
-            if (n < heads_here) {
-                const int64_t pi = part_base + n * part_stride;
-                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
-                float* dst = p.part_o + pi * D + 4 * j;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    *reinterpret_cast<float4*>(dst + 16 * dt) =
-                        make_float4(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv, a.o[nb][dt][2] * inv,
-                                    a.o[nb][dt][3] * inv);
-                }
-                if (j == 0) {
-                    p.part_lse[pi] = a.l[nb] > 0.f ? a.m[nb] + fast_log2(a.l[nb]) : kNegInf;
-                }
-            }
-        }
-    }
-
-    // Online-softmax merge of another wave's finished accumulator (same lane layout).
-    __device__ static void merge(Acc& a, const Acc& b) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const float m = fmaxf(a.m[nb], b.m[nb]);
-            const float sa = a.m[nb] == kNegInf ? 0.f : fast_exp2(a.m[nb] - m);
-            const float sb = b.m[nb] == kNegInf ? 0.f : fast_exp2(b.m[nb] - m);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = a.o[nb][dt] * sa + b.o[nb][dt] * sb;
-            }
-            a.l[nb] = a.l[nb] * sa + b.l[nb] * sb;
-            a.m[nb] = m;
-        }
-    }
-
-    // Accumulator through LDS, one float per lane and field (conflict-free).
-    static constexpr int kAccFloats = NB * (4 * DT + 2);
-    __device__ static void store_lds(const Acc& a, float* base, int lane) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            float* bb = base + nb * (4 * DT + 2) * 64;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    bb[(4 * dt + i) * 64 + lane] = a.o[nb][dt][i];
-                }
-            }
-            bb[4 * DT * 64 + lane] = a.m[nb];
-            bb[(4 * DT + 1) * 64 + lane] = a.l[nb];
-        }
-    }
-    __device__ static void load_lds(Acc& a, const float* base, int lane) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const float* bb = base + nb * (4 * DT + 2) * 64;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    a.o[nb][dt][i] = bb[(4 * dt + i) * 64 + lane];
-                }
-            }
-            a.m[nb] = bb[4 * DT * 64 + lane];
-            a.l[nb] = bb[(4 * DT + 1) * 64 + lane];
-        }
-    }
-};
-
-// ---------------------------------------------------------------- VALU math
-
-// 8-element dot product of two packed 16-bit vectors, accumulated in fp32.
-template <bool BF16>
-__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
-    c = dot2<BF16>(a.x, b.x, c);
-    c = dot2<BF16>(a.y, b.y, c);
-    c = dot2<BF16>(a.z, b.z, c);
-    return dot2<BF16>(a.w, b.w, c);
-}
-
-template <bool BF16, int D, int NH>
-struct ValuMath {
-    static constexpr int kHeads = NH;
-    static constexpr int E = D / 64; // output dims per lane and head
-    static constexpr bool kMultiQuery = false; // one query token, no mask
-
-    // Lane (t, c) = (lane & 15, lane >> 4): q of every head, dims 8(4i + c) .. +7.
-    struct Q {
-        uint4 q[NH][D / 32];
-    };
-    // Lane owns dims E * lane .. + E - 1 of every head.
-    struct Acc {
-        float o[NH][E];
-        float m[NH];
-        float l[NH];
-    };
-
-    __device__ static int64_t out_row(const PartitionParams& p, int b, int kvh, int r) {
-        return static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r;
-    }
-
-    __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int heads_here, int lane,
-                                  Q& q) {
-        const int c = lane >> 4;
-        const int64_t bh_first = out_row(p, b, kvh, r_first);
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-#pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                q.q[h][i] = h < heads_here
-                                ? *reinterpret_cast<const uint4*>(p.q + (bh_first + h) * D + 8 * (4 * i + c))
-                                : make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-    }
-
-    __device__ static void set_mask(const PartitionParams&, int, int, int, int, Q&) {}
-
-    __device__ static void init(Acc& a) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                a.o[h][e] = 0.f;
-            }
-            a.m[h] = kNegInf;
-            a.l[h] = 0.f;
-        }
-    }
-
-    __device__ static void tile(const Q& q, Acc& a, const uint16_t* lds, int t0, int end, int lane,
-                                float scale_log2) {
-        const int t = lane & 15;
-        const int c = lane >> 4;
-        // Scores: the same K addresses as the MFMA A operand (conflict-free).
-        uint4 kv[D / 32];
-        const uint16_t* kr = lds + t * VTile<D>::kRow + 8 * c;
-#pragma unroll
-        for (int i = 0; i < D / 32; ++i) {
-            kv[i] = *reinterpret_cast<const uint4*>(kr + 32 * i);
-        }
-        float pr[NH];
-        const bool valid = t0 + t < end;
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            float s = 0.f;
-#pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                s = dot8<BF16>(kv[i], q.q[h][i], s);
-            }
-            s = sum_halves32(sum_rows16(s)); // the four dim quarters of token t
-            const float sc = valid ? s * scale_log2 : kNegInf;
-            const float tmax = group_max<16>(sc); // over the 16 tokens (rows are identical)
-            if (tmax > a.m[h] + kLazyRescaleLog2) { // uniform: tmax and m are wave-wide values
-                const float m_new = tmax;
-                const float alpha = fast_exp2(a.m[h] - m_new);
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    a.o[h][e] *= alpha;
-                }
-                a.l[h] *= alpha;
-                a.m[h] = m_new;
-            }
-            pr[h] = fast_exp2(sc - a.m[h]);
-            a.l[h] += pr[h];
-        }
-        // O[h][d] += sum_t p[h][t] V[t][d]: lane owns dims E * lane .. + E - 1;
-        // p[h][t] comes from lane t with readlane.
-        const uint16_t* vt = lds + VTile<D>::kElems + E * lane;
-#pragma unroll
-        for (int tt = 0; tt < 16; ++tt) {
-            float vf[E];
-            if constexpr (E == 1) {
-                const uint32_t w = vt[tt * VTile<D>::kRow];
-                vf[0] = BF16 ? bf16_lo(w) : f16_lo(w);
-            } else if constexpr (E == 2) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(vt + tt * VTile<D>::kRow);
-                unpack2<BF16>(w, vf[0], vf[1]);
-            } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(vt + tt * VTile<D>::kRow);
-                unpack2<BF16>(w.x, vf[0], vf[1]);
-                unpack2<BF16>(w.y, vf[2], vf[3]);
-            }
-#pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                const float ph = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[h]), tt));
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    a.o[h][e] = fmaf(ph, vf[e], a.o[h][e]);
-                }
-            }
-        }
-    }
-
-    // l holds lane t's token sums; total over the 16 tokens of a row.
-    __device__ static void finish(Acc& a) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            a.l[h] = group_sum<16>(a.l[h]);
-        }
-    }
-
-    __device__ static void write_final(const PartitionParams& p, const Q&, int64_t bh_first, int heads_here,
-                                       const Acc& a, int lane) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            if (h < heads_here) {
-                const float inv = a.l[h] > 0.f ? 1.f / a.l[h] : 0.f;
-                uint16_t* dst = p.out + (bh_first + h) * D + E * lane;
-                if constexpr (E == 1) {
-                    dst[0] = from_f32<BF16>(a.o[h][0] * inv);
-                } else if constexpr (E == 2) {
-                    *reinterpret_cast<uint32_t*>(dst) = pack2<BF16>(a.o[h][0] * inv, a.o[h][1] * inv);
-                } else {
-                    uint2 w;
-                    w.x = pack2<BF16>(a.o[h][0] * inv, a.o[h][1] * inv);
-                    w.y = pack2<BF16>(a.o[h][2] * inv, a.o[h][3] * inv);
-                    *reinterpret_cast<uint2*>(dst) = w;
-                }
-            }
-        }
-    }
-
-    __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
-                                         int heads_here, const Acc& a, int lane) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            if (h < heads_here) {
-                const int64_t pi = part_base + h * part_stride;
-                const float inv = a.l[h] > 0.f ? 1.f / a.l[h] : 0.f;
-                float* dst = p.part_o + pi * D + E * lane;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    dst[e] = a.o[h][e] * inv;
-                }
-                if (lane == 0) {
-                    p.part_lse[pi] = a.l[h] > 0.f ? a.m[h] + fast_log2(a.l[h]) : kNegInf;
-                }
-            }
-        }
-    }
-
-    // Online-softmax merge of another wave's finished accumulator (same lane layout).
-    __device__ static void merge(Acc& a, const Acc& b) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-            const float m = fmaxf(a.m[h], b.m[h]);
-            const float sa = a.m[h] == kNegInf ? 0.f : fast_exp2(a.m[h] - m);
-            const float sb = b.m[h] == kNegInf ? 0.f : fast_exp2(b.m[h] - m);
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                a.o[h][e] = a.o[h][e] * sa + b.o[h][e] * sb;
-            }
-            a.l[h] = a.l[h] * sa + b.l[h] * sb;
-            a.m[h] = m;
-        }
-    }
-
-    // Accumulator through LDS, one float per lane and field (conflict-free).
-    static constexpr int kAccFloats = NH * (E + 2);
-    __device__ static void store_lds(const Acc& a, float* base, int lane) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                base[(h * E + e) * 64 + lane] = a.o[h][e];
-            }
-            base[(NH * E + h) * 64 + lane] = a.m[h];
-            base[(NH * E + NH + h) * 64 + lane] = a.l[h];
-        }
-    }
-    __device__ static void load_lds(Acc& a, const float* base, int lane) {
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                a.o[h][e] = base[(h * E + e) * 64 + lane];
-            }
-            a.m[h] = base[(NH * E + h) * 64 + lane];
-            a.l[h] = base[(NH * E + NH + h) * 64 + lane];
-        }
-    }
-};
-
-// ---------------------------------------------------------------- tile pipeline
-
-// Walks the tiles of [t, end) with DEPTH tiles of loads in flight.  RELOAD
-// adds the page-window refresh for ranges longer than 64 pages (a dependent
-// global load, so it drains the pipeline once per 64 pages); the common path
-// has none and every prefetch is unconditional, so all waits are exact.
-template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD>
-__device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_t* __restrict__ bt_row, int last_page,
-                                          int& win, int& win_base, const typename Math::Q& q,
-                                          typename Math::Acc& acc, uint16_t* lds, int t, int end, int lane,
-                                          int kvh) {
-    auto ensure_window = [&](int tn) {
-        if constexpr (RELOAD) {
-            const int tl = min(tn + 15, end - 1);
-            if (tn < end && (tl >> p.page_shift) - win_base >= 64) {
-                win_base = tn >> p.page_shift;
-                win = load_page_window(bt_row, win_base, last_page, threadIdx.x & 63, p.num_pages);
-            }
-        }
-    };
-    // Counted loops without a mid-body exit: a `break` between the two halves
-    // would be structurized through the loop header and make the compiler's
-    // wait counts assume the just-issued prefetch is the tile being consumed.
-    const int ntiles = (end - t + 15) >> 4;
-    // Per tile: stage the landed tile in LDS, immediately issue the prefetch
-    // into the freed registers (pinned there by a scheduling barrier), then
-    // compute.  The prefetch is in flight for the whole QK / softmax / PV.
-    TileRegs<D> ra;
-    load_tile<D, WIDE>(ra, p, win, win_base, t, end, true, lane, kvh);
-    if constexpr (DEPTH == 1) {
-        for (int k = 0; k < ntiles; ++k) {
-            stage_tile<D>(ra, lds, lane);
-            ensure_window(t + 16);
-            load_tile<D, WIDE>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
-            __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
-            t += 16;
-        }
-    } else {
-        TileRegs<D> rb;
-        ensure_window(t + 16);
-        load_tile<D, WIDE>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
-        for (int k = 0; k + 2 <= ntiles; k += 2) {
-            stage_tile<D>(ra, lds, lane);
-            ensure_window(t + 32);
-            load_tile<D, WIDE>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
-            __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
-            t += 16;
-            stage_tile<D>(rb, lds, lane);
-            ensure_window(t + 32);
-            load_tile<D, WIDE>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
-            __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
-            t += 16;
-        }
-        if (ntiles & 1) {
-            stage_tile<D>(ra, lds, lane);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
-        }
-    }
-}
-
-// Attention of one head slice over tokens [begin, end) (begin < end), the page
-// window already loaded at win_base = begin / P.  Leaves Math's accumulator
-// (unnormalised O, reference max, denominator) finished.
-template <typename Math, int D, bool WIDE, int DEPTH>
-__device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
-                                             int win_base, const typename Math::Q& q, uint16_t* lds, int begin,
-                                             int end, int lane, int kvh, typename Math::Acc& acc) {
-    Math::init(acc);
-    const int last_page = (end - 1) >> p.page_shift;
-    if (last_page - win_base < 64) {
-        // Common case: the whole range fits in one page window.
-        tile_loop<Math, D, WIDE, DEPTH, false>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end, lane,
-                                               kvh);
-    } else {
-        tile_loop<Math, D, WIDE, DEPTH, true>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end, lane,
-                                              kvh);
-    }
-    Math::finish(acc);
-}
-
-// Split schedules (one split, page-balanced splits, token windows): one wave
-// per work item (b, kv head, head group, split).
-template <typename Math, int D, bool WIDE, int DEPTH>
-__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
-void partition_split_kernel(PartitionParams p) {
-    constexpr int kWaves = kWavesPerGroup;
-    static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
-    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][2 * VTile<D>::kElems];
-
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int item = wave_item();
-    if (item >= p.num_items) {
-        return;
-    }
-    const Item it = decode_item(item, p);
-    const int split = it.split;
-    const int b = it.b;
-    const int kvh = it.kvh;
-    const int hg = it.hg;
-
-    const int r_first = hg * Math::kHeads;
-    const int heads_here = min(Math::kHeads, p.rows - r_first);
-    const int64_t bh_first = Math::out_row(p, b, kvh, r_first);
-    // Partials are indexed by query row of (b, kv head): the output row index
-    // itself when there is one query token.
-    const int64_t sr_first = (static_cast<int64_t>(b) * p.num_heads_k + kvh) * p.rows + r_first;
-
-    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-
-    // q and, with token windows, the page window do not depend on
-    // cache_seqlens, so their loads are issued together with its load: the
-    // item prologue costs two dependent round trips instead of three.
-    typename Math::Q q;
-    Math::load_q(p, b, kvh, r_first, heads_here, lane, q);
-    const bool windowed = p.split_tokens > 0;
-    int win_base = 0;
-    int win = 0;
-    if (windowed) {
-        // Entries past the row's last page are loaded too (ids are clamped to
-        // the pool) but never used for a valid token.
-        win_base = (split * p.split_tokens) >> p.page_shift;
-        win = load_page_window(bt_row, win_base, p.bt_stride - 1, lane, p.num_pages);
-    }
-
-    const int seqlen = min(p.seqlens[b], p.row_cap);
-    Math::set_mask(p, b, seqlen, heads_here, lane, q);
-    const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
-
-    if (range.begin >= range.end) {
-        // Empty range.  With one split the row has no tokens: its output is 0.
-        // With several, the combine derives each row's non-empty splits from
-        // cache_seqlens and never reads this item's slot, so nothing is written.
-        if (p.splits == 1) {
-            constexpr int CH = D / 8; // 16-byte output chunks per row
-            for (int idx = lane; idx < heads_here * CH; idx += 64) {
-                const int g = idx / CH;
-                const int c = idx % CH;
-                *reinterpret_cast<uint4*>(p.out + Math::out_row(p, b, kvh, r_first + g) * D + c * 8) =
-                    make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-        return;
-    }
-    if (!windowed) {
-        win_base = range.begin >> p.page_shift;
-        win = load_page_window(bt_row, win_base, (range.end - 1) >> p.page_shift, lane, p.num_pages);
-    }
-
-    typename Math::Acc acc;
-    attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], range.begin, range.end, lane,
-                                       kvh, acc);
-    if (p.splits == 1) {
-        Math::write_final(p, q, bh_first, heads_here, acc, lane);
-    } else {
-        Math::write_partial(p, sr_first * p.splits + split, p.splits, heads_here, acc, lane);
-    }
-}
-
-// Split schedules with fewer items than CUs (small batches): one workgroup per
-// item, its waves taking consecutive quarters of the item's tiles; each wave
-// then parks its finished accumulator in its own LDS tile and wave 0 merges
-// the four (online-softmax merge) and writes the item's output or partial.
-// Still one pass per item and no workspace: only the latency changes.
-template <typename Math, int D, bool WIDE, int DEPTH>
-__global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
-void partition_item_group_kernel(PartitionParams p) {
-    constexpr int kWaves = kWavesPerGroup;
-    // Each wave's LDS holds its K/V tiles, and afterwards its parked accumulator.
-    constexpr int kWaveElems = Math::kAccFloats * 64 * 2 > 2 * VTile<D>::kElems ? Math::kAccFloats * 64 * 2
-                                                                                : 2 * VTile<D>::kElems;
-    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][kWaveElems];
-
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const Item it = decode_item(static_cast<int32_t>(blockIdx.x), p);
-    const int r_first = it.hg * Math::kHeads;
-    const int heads_here = min(Math::kHeads, p.rows - r_first);
-    const int64_t bh_first = Math::out_row(p, it.b, it.kvh, r_first);
-    const int64_t sr_first = (static_cast<int64_t>(it.b) * p.num_heads_k + it.kvh) * p.rows + r_first;
-    const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(it.b) * p.bt_stride;
-
-    typename Math::Q q;
-    Math::load_q(p, it.b, it.kvh, r_first, heads_here, lane, q);
-    const int seqlen = min(p.seqlens[it.b], p.row_cap);
-    Math::set_mask(p, it.b, seqlen, heads_here, lane, q);
-    const TokenRange range = split_tokens_of(seqlen, p.page_shift, it.split, p.splits, p.split_tokens);
-    if (range.begin >= range.end) {
-        // As in partition_split_kernel: zeros for an empty row, nothing for an empty split.
-        if (p.splits == 1 && wave == 0) {
-            constexpr int CH = D / 8;
-            for (int idx = lane; idx < heads_here * CH; idx += 64) {
-                const int g = idx / CH;
-                const int c = idx % CH;
-                *reinterpret_cast<uint4*>(p.out + Math::out_row(p, it.b, it.kvh, r_first + g) * D + c * 8) =
-                    make_uint4(0u, 0u, 0u, 0u);
-            }
-        }
-        return;
-    }
-    const int ntiles = (range.end - range.begin + 15) >> 4;
-    const int per = (ntiles + kWaves - 1) / kWaves;
-    const int sub_begin = range.begin + 16 * min(ntiles, wave * per);
-    const int sub_end = min(range.end, range.begin + 16 * min(ntiles, (wave + 1) * per));
-
-    typename Math::Acc acc;
-    if (sub_begin < sub_end) {
-        const int win_base = sub_begin >> p.page_shift;
-        const int win = load_page_window(bt_row, win_base, (sub_end - 1) >> p.page_shift, lane, p.num_pages);
-        attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], sub_begin, sub_end, lane,
-                                           it.kvh, acc);
-    } else {
-        Math::init(acc);
-        Math::finish(acc);
-    }
-    Math::store_lds(acc, reinterpret_cast<float*>(lds_tiles[wave]), lane);
-    __syncthreads();
-    if (wave != 0) {
-        return;
-    }
-#pragma unroll
-    for (int k = 1; k < kWaves; ++k) {
-        typename Math::Acc other;
-        Math::load_lds(other, reinterpret_cast<const float*>(lds_tiles[k]), lane);
-        Math::merge(acc, other);
-    }
-    if (p.splits == 1) {
-        Math::write_final(p, q, bh_first, heads_here, acc, lane);
-    } else {
-        Math::write_partial(p, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane);
-    }
-}
-
-// Tile-balanced schedule (streams, units, shares and slots as defined with
-// row_tiles and make_tile_plan in pkv_device.h): wave w streams its share,
-// segment by segment.  A segment that is a whole stream is written to the
-// output; any other leaves a partial in slot w + r for the combine.  The workgroup's LDS request is padded on the
-// host so that one workgroup occupies a CU: the dispatcher then spreads the
-// grid over all CUs instead of doubling some up while others idle.
-template <typename Math, int D, bool WIDE, int DEPTH, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[WAVES][2 * VTile<D>::kElems];
-
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int32_t w = static_cast<int32_t>(blockIdx.x) * WAVES + wave;
-    if (w >= p.tile_workers) {
-        return;
-    }
-    const int32_t spr = p.num_heads_k * p.head_groups;
-    const RowScan scan = scan_rows(p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left, lane);
-    const TilePlan plan = make_tile_plan(static_cast<int64_t>(spr) * uniform(scan.rows_total), p.tile_workers);
-    if (w >= plan.workers) {
-        return;
-    }
-    uint16_t* lds = lds_tiles[wave];
-
-    // Streams the tiles among this worker's units [x0, x_end), stream by
-    // stream; partials go to slot w + r.
-    auto run_share = [&](int64_t x0, int64_t x_end) {
-        const RowTiles rt = locate_unit_row(scan, p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left,
-                                            muldiv(x0, 1, spr), lane);
-        int b = uniform(rt.b);
-        int seqlen = uniform(rt.seqlen);
-        int nb = uniform(rt.n);
-        int first = tile_span(seqlen, p.q_len, p.win_left).first;
-        int units = stream_units(nb);
-        const int64_t row_first = static_cast<int64_t>(spr) * uniform(rt.before); // first unit of row b
-        int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));
-        int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
-        while (true) {
-            // The share's tiles of stream (b, u): units [x0, x_end) minus the header.
-            const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
-            const int t_hi = static_cast<int>(min(static_cast<int64_t>(nb), x_end - vs - kHeaderTiles));
-            if (t_lo < t_hi) {
-                const int kvh = u / p.head_groups;
-                const int hg = u - kvh * p.head_groups;
-                const int r_first = hg * Math::kHeads;
-                const int heads_here = min(Math::kHeads, p.rows - r_first);
-                const int64_t bh_first = Math::out_row(p, b, kvh, r_first);
-                const int32_t* __restrict__ bt_row = p.block_table + static_cast<int64_t>(b) * p.bt_stride;
-                const int begin = (first + t_lo) * 16;
-                const int end = min((first + t_hi) * 16, seqlen);
-
-                typename Math::Q q;
-                Math::load_q(p, b, kvh, r_first, heads_here, lane, q);
-                Math::set_mask(p, b, seqlen, heads_here, lane, q);
-                const int win_base = begin >> p.page_shift;
-                const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
-
-                typename Math::Acc acc;
-                attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc);
-                if (t_lo == 0 && t_hi == nb) {
-                    Math::write_final(p, q, bh_first, heads_here, acc, lane);
-                } else {
-                    const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
-                    Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane);
-                }
-            }
-            vs += units;
-            if (vs >= x_end) {
-                break;
-            }
-            // Next stream, past rows without tokens (they own no units).
-            if (++u == spr) {
-                u = 0;
-                do {
-                    ++b;
-                    seqlen = uniform(clamped_seqlen(p.seqlens, b, p.row_cap));
-                } while (seqlen == 0 && b + 1 < p.batch);
-                const TileSpan span = tile_span(seqlen, p.q_len, p.win_left);
-                first = span.first;
-                nb = span.n;
-                units = stream_units(nb);
-            }
-        }
-    };
-
-    run_share(share_start(w, plan), share_start(w + 1, plan));
-}
-
-// Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
-// whole chip busy and streams fastest with one; split schedules with fewer
-// items than CUs are latency-bound and take two.
-#ifndef PKV_MFMA_DEPTH
-#define PKV_MFMA_DEPTH 1
-#endif
-constexpr int kSplitDepthFewItems = 2;
-
-template <typename Math, int D, bool WIDE>
-static void launch_tiles(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    constexpr int kWaves = kTileWaves;
-    const int blocks = (p.tile_workers + kWaves - 1) / kWaves;
-    // More than half of the CU's 160 KB of LDS per workgroup: at most one
-    // workgroup per CU.
-    constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
-    constexpr size_t kHalf = 80 * 1024;
-    const size_t dyn = kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
-    launch_kernel(partition_tiles_kernel<Math, D, WIDE, PKV_MFMA_DEPTH, kWaves>, dim3(blocks), dim3(64 * kWaves), dyn,
-                  stream, ev, p);
-}
-
-template <typename Math, int D, bool WIDE>
-static void launch_split(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    const dim3 block(64 * kWavesPerGroup);
-    if (p.num_items < kComputeUnits) {
-        // Fewer items than CUs: a workgroup per item, latency-bound, two tiles in flight.
-        launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems>, dim3(p.num_items), block, 0,
-                      stream, ev, p);
-    } else {
-        launch_kernel(partition_split_kernel<Math, D, WIDE, PKV_MFMA_DEPTH>, dim3(p.num_groups), block, 0, stream,
-                      ev, p);
-    }
-}
-
-template <typename Math, int D>
-static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
-    const bool wide = p.page_shift >= 4;
-    if (p.tile_workers > 0) {
-        if (wide) {
-            launch_tiles<Math, D, true>(p, stream, ev);
-        } else {
-            launch_tiles<Math, D, false>(p, stream, ev);
-        }
-    } else if (wide) {
-        launch_split<Math, D, true>(p, stream, ev);
-    } else {
-        launch_split<Math, D, false>(p, stream, ev);
-    }
-    return hipGetLastError();
-}
-
-template <bool BF16, int D>
-static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wave, hipStream_t stream,
-                           const LaunchEvents& ev) {
-    const bool multi_query = p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr;
-    if (mfma) {
-        // 16 or 32 query rows per wave (heads_per_wave).
-        if (heads_per_wave == 32) {
-            if (multi_query) {
-                return launch_math<MfmaMath<BF16, D, true, 2>, D>(p, stream, ev);
-            }
-            return launch_math<MfmaMath<BF16, D, false, 2>, D>(p, stream, ev);
-        }
-        if (multi_query) {
-            return launch_math<MfmaMath<BF16, D, true, 1>, D>(p, stream, ev);
-        }
-        return launch_math<MfmaMath<BF16, D, false, 1>, D>(p, stream, ev);
-    }
-    if (multi_query) {
-        return hipErrorInvalidValue; // the VALU policy has one query token and no mask
-    }
-    switch (heads_per_wave) {
-    case 1: return launch_math<ValuMath<BF16, D, 1>, D>(p, stream, ev);
-    case 2: return launch_math<ValuMath<BF16, D, 2>, D>(p, stream, ev);
-    case 4: return launch_math<ValuMath<BF16, D, 4>, D>(p, stream, ev);
-    default: return hipErrorInvalidValue;
-    }
-}
+hipError_t launch_partition_d64(const PartitionParams& p, bool mfma, bool bf16, int heads_per_wave,
+                                hipStream_t stream, const LaunchEvents& ev);
+hipError_t launch_partition_d128(const PartitionParams& p, bool mfma, bool bf16, int heads_per_wave,
+                                 hipStream_t stream, const LaunchEvents& ev);
+hipError_t launch_partition_d256(const PartitionParams& p, bool mfma, bool bf16, int heads_per_wave,
+                                 hipStream_t stream, const LaunchEvents& ev);
 
 hipError_t launch_partition(const PartitionParams& p, bool mfma, bool bf16, int head_dim, int heads_per_wave,
                             hipStream_t stream, const LaunchEvents& ev) {
-    if (bf16) {
-        switch (head_dim) {
-        case 64: return launch_d<true, 64>(p, mfma, heads_per_wave, stream, ev);
-        case 128: return launch_d<true, 128>(p, mfma, heads_per_wave, stream, ev);
-        case 256: return launch_d<true, 256>(p, mfma, heads_per_wave, stream, ev);
-        default: return hipErrorInvalidValue;
-        }
-    }
     switch (head_dim) {
-    case 64: return launch_d<false, 64>(p, mfma, heads_per_wave, stream, ev);
-    case 128: return launch_d<false, 128>(p, mfma, heads_per_wave, stream, ev);
-    case 256: return launch_d<false, 256>(p, mfma, heads_per_wave, stream, ev);
+    case 64: return launch_partition_d64(p, mfma, bf16, heads_per_wave, stream, ev);
+    case 128: return launch_partition_d128(p, mfma, bf16, heads_per_wave, stream, ev);
+    case 256: return launch_partition_d256(p, mfma, bf16, heads_per_wave, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }

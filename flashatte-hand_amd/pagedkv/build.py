@@ -23,7 +23,8 @@ LIB_PATH = LIB_DIR / "libpkv_decode.so"
 ORACLE_DIR = REPO_ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "libpkv_oracle.so"
 
-SOURCES = ["pkv_partition.hip", "pkv_combine.hip", "pkv_append.hip", "pkv_api.cpp"]
+SOURCES = ["pkv_part_d128.hip", "pkv_part_d256.hip", "pkv_part_d64.hip", "pkv_partition.hip",
+           "pkv_combine.hip", "pkv_append.hip", "pkv_api.cpp"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -57,7 +58,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def build_library(verbose: bool = False, jobs: int = 4, out: Path | None = None,
+def build_library(verbose: bool = False, jobs: int = 0, out: Path | None = None,
                   defines: tuple[str, ...] = ()) -> Path:
     """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds).
 
@@ -74,7 +75,9 @@ def build_library(verbose: bool = False, jobs: int = 4, out: Path | None = None,
         lang = ["-x", "hip"]
         cmds.append([hipcc, *HIPCC_FLAGS, *[f"-D{d}" for d in defines], *lang, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+    if jobs <= 0:
+        jobs = min(len(cmds), max(1, min(16, os.cpu_count() or 1)))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = lib_path.with_suffix(".so.tmp")
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
