@@ -97,6 +97,14 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     cfg = make_config(name)
     sets = [make_tensors(cfg, "cuda", seed=cfg.seed + 7919 * i) for i in range(max(1, args.sets))]
     M = max(1, args.seqlen_q)
+    fp8 = args.kv == "fp8"
+    if fp8:
+        # OCP FP8 e4m3 caches with per-KV-head scales: the same shapes at one byte per element.
+        for s_ in sets:
+            for name in ("k_cache", "v_cache"):
+                s_[name] = s_[name].float().clamp(-448, 448).to(torch.float8_e4m3fn)
+            s_["k_scale"] = torch.rand(cfg.num_heads_k, device="cuda") + 0.5
+            s_["v_scale"] = torch.rand(cfg.num_heads_k, device="cuda") + 0.5
     if M > 1:
         # Several query tokens per row (speculative-decode verify): q / out [B, M, H, D].
         for s_ in sets:
@@ -113,6 +121,8 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
         max_seqlen=int(cfg.seqlens.max()), path=args.path, split_tokens=args.split_tokens,
         seqlen_q=M, causal=args.causal, window_size=tuple(args.window),
+        kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
+        k_scale=base["k_scale"].data_ptr() if fp8 else 0, v_scale=base["v_scale"].data_ptr() if fp8 else 0,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
@@ -133,6 +143,9 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     def call(i, ev_ptr=None):
         q, k, v, bt, sl, o = ptrs[i % len(ptrs)]
         desc.prof_events = ev_ptr
+        if fp8:
+            desc.k_scale = sets[i % len(sets)]["k_scale"].data_ptr()
+            desc.v_scale = sets[i % len(sets)]["v_scale"].data_ptr()
         st = lib.pkv_decode(q, k, v, bt, sl, scale, splits_req, o, ctypes.byref(desc), sh)
         if st != 0:
             raise pagedkv.PkvError(st)
@@ -164,12 +177,13 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     events.destroy([t_start, t_end])
 
     ms_per_step = total_ms / K
-    kv_bytes = cfg.kv_bytes()
+    kv_elem = 1 if fp8 else cfg.elem_bytes
+    kv_bytes = cfg.kv_bytes() // cfg.elem_bytes * kv_elem
     if args.window[0] >= 0:
         # A left window leaves each row the keys from L - M - left on.
         L = cfg.seqlens.clip(min=0).astype(np.int64)
         span = L - np.clip(L - M - args.window[0], 0, None)
-        kv_bytes = int(span.sum()) * cfg.num_heads_k * D * 2 * cfg.elem_bytes
+        kv_bytes = int(span.sum()) * cfg.num_heads_k * D * 2 * kv_elem
     # Algorithmic bytes of one partition launch: valid K/V rows + q + block-table entries + seqlens
     # (the output is written by the combine kernel and is not counted here).
     part_alg = cfg.total_bytes() - cfg.batch * cfg.num_heads * D * cfg.elem_bytes
@@ -178,7 +192,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     part_avg_ms = sum(part_ms) / K
     achieved = part_alg / (part_avg_ms * 1e-3) / 1e9
     # The committed counter summary is for the one-query, unmasked decode.
-    plain = M == 1 and tuple(args.window) == (-1, -1)
+    plain = M == 1 and tuple(args.window) == (-1, -1) and not fp8
     traffic = load_traffic(name, "mfma" if path == pagedkv.PKV_PATH_MFMA else "valu") if plain else None
     res = {
         "config": cfg,
@@ -400,6 +414,9 @@ def main() -> int:
     ap.add_argument("--causal", action="store_true", help="causal mask (decode op, with --seqlen-q > 1)")
     ap.add_argument("--window", type=int, nargs=2, default=(-1, -1), metavar=("LEFT", "RIGHT"),
                     help="sliding window (decode op); -1 = unbounded")
+    ap.add_argument("--kv", choices=("same", "fp8"), default="same",
+                    help="KV cache element type (decode op): the config's 16-bit dtype, or OCP FP8 e4m3 with "
+                         "per-KV-head scales")
     ap.add_argument("--op", choices=("decode", "append", "decode_append"), default="decode",
                     help="decode (default, the headline); append: paged KV-cache append; decode_append: "
                          "decode with one new token per row appended in the call")
@@ -455,7 +472,8 @@ def main() -> int:
                        "split_tokens": res["split_tokens"],
                        "path": res["path"], "kv_sets": args.sets,
                        **({"seqlen_q": args.seqlen_q, "causal": args.causal} if args.seqlen_q > 1 else {}),
-                       **({"window": list(args.window)} if tuple(args.window) != (-1, -1) else {})},
+                       **({"window": list(args.window)} if tuple(args.window) != (-1, -1) else {}),
+                       **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {})},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
             "hbm_frac_kv": round(res["kv_gbps"] / HBM_PEAK_GBPS, 4),
@@ -465,7 +483,8 @@ def main() -> int:
             "roofline": res["roofline"],
             "cpu_baseline": None,
         }
-        if name == args.config and not args.no_cpu:
+        # The CPU baseline restates the reference's own path: 16-bit caches, one query token.
+        if name == args.config and not args.no_cpu and args.kv == "same" and args.seqlen_q == 1:
             line["cpu_baseline"] = cpu_baseline(res, torch, args.cpu_budget)
         res.pop("host_arrays", None)
         lines.append(line)

@@ -34,6 +34,7 @@ struct Resolved {
     int win_left;     // -1 = unbounded
     int win_right;    // -1 = unbounded (0 with a causal mask and several query tokens)
     bool multi_query; // several query tokens, a window or ALiBi: the masked MFMA policy
+    bool kv_fp8;      // caches hold OCP FP8 e4m3
     int page_shift;
     int heads_per_wave;
     int head_groups;
@@ -90,8 +91,11 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (d->path != PKV_PATH_AUTO && d->path != PKV_PATH_VALU && d->path != PKV_PATH_MFMA) {
         return PKV_EINVAL;
     }
-    if (d->split_tokens < 0 || d->split_tokens % 16 != 0 || d->reserved != 0 || d->reserved2 != 0) {
+    if (d->split_tokens < 0 || d->split_tokens % 16 != 0 || d->reserved != 0) {
         return PKV_EINVAL;
+    }
+    if (d->kv_dtype != PKV_KV_DTYPE_SAME && d->kv_dtype != PKV_KV_DTYPE_FP8_E4M3) {
+        return PKV_EUNSUPPORTED;
     }
     if (d->seqlen_q < 0 || (d->mask & ~(PKV_MASK_CAUSAL | PKV_MASK_WINDOW)) != 0 || d->alibi_batch_stride < 0) {
         return PKV_EINVAL;
@@ -129,9 +133,10 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     const int64_t row_cap = d->block_table_stride * r.P;
     const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
     r.max_pages = std::max<int64_t>(1, (max_seqlen + r.P - 1) / r.P);
+    r.kv_fp8 = d->kv_dtype == PKV_KV_DTYPE_FP8_E4M3;
     r.path = d->path == PKV_PATH_AUTO ? auto_path(r) : d->path;
-    if (r.multi_query && r.path != PKV_PATH_MFMA) {
-        return PKV_EUNSUPPORTED; // the VALU policy has one query token and no mask
+    if ((r.multi_query || r.kv_fp8) && r.path != PKV_PATH_MFMA) {
+        return PKV_EUNSUPPORTED; // the VALU policy has one query token, no mask and 16-bit caches
     }
     // MFMA: one block of 16 query rows per wave, or two when a KV head has
     // more than 16 (the K/V tile is then read once for 32 rows).
@@ -306,6 +311,9 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.win_right = r.win_right;
     p.alibi = desc->alibi_slopes;
     p.alibi_stride = desc->alibi_batch_stride;
+    p.kv_fp8 = r.kv_fp8 ? 1 : 0;
+    p.k_scale = desc->k_scale;
+    p.v_scale = desc->v_scale;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -370,6 +378,11 @@ pkv::AppendParams append_params(const Resolved& r, const pkv_decode_desc* d, con
     a.bt_stride = static_cast<int32_t>(d->block_table_stride);
     a.num_pages = static_cast<int32_t>(d->num_pages);
     a.batch = static_cast<int32_t>(r.B);
+    a.kv_fp8 = r.kv_fp8 ? 1 : 0;
+    a.bf16 = d->dtype == PKV_DTYPE_BF16 ? 1 : 0;
+    a.head_chunks = static_cast<int32_t>(r.D / 8);
+    a.k_scale = d->k_scale;
+    a.v_scale = d->v_scale;
     return a;
 }
 

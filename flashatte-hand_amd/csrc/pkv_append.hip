@@ -17,6 +17,8 @@
 //    page * P + slot; a negative slot is padding and is skipped.
 // Positions past the block-table row, page ids outside [0, num_pages) and slots
 // outside the cache are not written, so a bad index never writes out of bounds.
+// FP8 caches (OCP e4m3) store each value quantised with its KV head's scale:
+// e4m3(sat(x * (1 / scale))), ties to even, saturated to +-448.
 #include <algorithm>
 
 #include "pkv_device.h"
@@ -77,7 +79,34 @@ __device__ __forceinline__ int64_t append_dst(const AppendParams& p, int64_t x) 
     return slot * p.chunks + c;
 }
 
-template <bool SLOTS>
+// Eight 16-bit values to eight OCP FP8 e4m3 bytes: x * inv in fp32, saturated
+// to +-448 (the conversion itself does not saturate), rounded to nearest even.
+template <bool BF16>
+__device__ __forceinline__ uint2 quantize8(const u32x4& x, float inv) {
+    float f[8];
+    unpack2<BF16>(x.x, f[0], f[1]);
+    unpack2<BF16>(x.y, f[2], f[3]);
+    unpack2<BF16>(x.z, f[4], f[5]);
+    unpack2<BF16>(x.w, f[6], f[7]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float y = f[e] * inv;
+        f[e] = fabsf(y) > 448.f ? copysignf(448.f, y) : y;
+    }
+    uint2 r;
+    r.x = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false));
+    r.x = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], static_cast<int>(r.x), true));
+    r.y = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], 0, false));
+    r.y = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], static_cast<int>(r.y), true));
+    return r;
+}
+
+// Reciprocal of the chunk's KV head scale (1 without scales).
+__device__ __forceinline__ float inv_scale(const float* scale, int32_t c, int32_t head_chunks) {
+    return scale != nullptr ? 1.0f / scale[c / head_chunks] : 1.0f;
+}
+
+template <bool SLOTS, bool FP8, bool BF16>
 __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendParams p) {
     constexpr int U = kAppendUnroll;
     const int64_t total = p.tokens * p.chunks;
@@ -86,6 +115,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendParams p) 
     const u32x4* v_new = reinterpret_cast<const u32x4*>(p.v_new);
     u32x4* k_cache = reinterpret_cast<u32x4*>(p.k_cache);
     u32x4* v_cache = reinterpret_cast<u32x4*>(p.v_cache);
+    uint2* k_cache8 = reinterpret_cast<uint2*>(p.k_cache);
+    uint2* v_cache8 = reinterpret_cast<uint2*>(p.v_cache);
     for (int64_t x0 = static_cast<int64_t>(blockIdx.x) * span + threadIdx.x; x0 < total;
          x0 += static_cast<int64_t>(gridDim.x) * span) {
         u32x4 kx[U];
@@ -108,9 +139,16 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendParams p) 
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (dst[u] >= 0) {
-                // Streaming stores: 3-4 % faster than cached ones on a prefill-sized append.
-                __builtin_nontemporal_store(kx[u], k_cache + dst[u]);
-                __builtin_nontemporal_store(vx[u], v_cache + dst[u]);
+                if constexpr (FP8) {
+                    // dst is the chunk index; its KV head is (dst % chunks) / head_chunks.
+                    const int32_t c = static_cast<int32_t>(dst[u] % p.chunks);
+                    k_cache8[dst[u]] = quantize8<BF16>(kx[u], inv_scale(p.k_scale, c, p.head_chunks));
+                    v_cache8[dst[u]] = quantize8<BF16>(vx[u], inv_scale(p.v_scale, c, p.head_chunks));
+                } else {
+                    // Streaming stores: 3-4 % faster than cached ones on a prefill-sized append.
+                    __builtin_nontemporal_store(kx[u], k_cache + dst[u]);
+                    __builtin_nontemporal_store(vx[u], v_cache + dst[u]);
+                }
             }
         }
     }
@@ -122,13 +160,26 @@ hipError_t launch_append(const AppendParams& p, hipStream_t stream, const Launch
         return hipSuccess;
     }
     const int64_t span = int64_t{kAppendThreads} * kAppendUnroll;
-    const int64_t groups = std::min<int64_t>((total + span - 1) / span, kAppendMaxGroups);
-    if (p.slot_mapping != nullptr) {
-        launch_kernel(append_kernel<true>, dim3(static_cast<uint32_t>(groups)), dim3(kAppendThreads), 0, stream, ev,
-                      p);
+    const dim3 grid(static_cast<uint32_t>(std::min<int64_t>((total + span - 1) / span, kAppendMaxGroups)));
+    const dim3 block(kAppendThreads);
+    const bool slots = p.slot_mapping != nullptr;
+    if (!p.kv_fp8) {
+        // A 16-bit copy does not depend on the dtype.
+        if (slots) {
+            launch_kernel(append_kernel<true, false, true>, grid, block, 0, stream, ev, p);
+        } else {
+            launch_kernel(append_kernel<false, false, true>, grid, block, 0, stream, ev, p);
+        }
+    } else if (p.bf16) {
+        if (slots) {
+            launch_kernel(append_kernel<true, true, true>, grid, block, 0, stream, ev, p);
+        } else {
+            launch_kernel(append_kernel<false, true, true>, grid, block, 0, stream, ev, p);
+        }
+    } else if (slots) {
+        launch_kernel(append_kernel<true, true, false>, grid, block, 0, stream, ev, p);
     } else {
-        launch_kernel(append_kernel<false>, dim3(static_cast<uint32_t>(groups)), dim3(kAppendThreads), 0, stream, ev,
-                      p);
+        launch_kernel(append_kernel<false, true, false>, grid, block, 0, stream, ev, p);
     }
     return hipGetLastError();
 }

@@ -49,6 +49,11 @@ struct PartitionParams {
     int32_t win_right;    // keys j <= pos + win_right; -1 = unbounded (0 when causal)
     const float* alibi;   // fp32 slopes at alibi[b * alibi_stride + h], or null
     int64_t alibi_stride;
+    // Cache element type: 0 = the compute dtype (16-bit), 1 = OCP FP8 e4m3
+    // (k / v then point at bytes) with per-KV-head fp32 scales (null = 1).
+    int32_t kv_fp8;
+    const float* k_scale;
+    const float* v_scale;
 };
 
 struct CombineParams {
@@ -95,6 +100,13 @@ struct AppendParams {
     int32_t bt_stride;
     int32_t num_pages;
     int32_t batch;
+    // FP8 caches: each 16-bit input value x is stored as e4m3(sat(x * (1 / scale)))
+    // with the chunk's KV head scale (chunk c belongs to head c / head_chunks).
+    int32_t kv_fp8;
+    int32_t bf16;                 // input dtype: 1 bf16, 0 fp16
+    int32_t head_chunks;          // 16-byte input chunks per KV head (D / 8)
+    const float* k_scale;         // [Hk] or null (1)
+    const float* v_scale;
 };
 
 constexpr float kNegInf = -__builtin_huge_valf();

@@ -64,10 +64,16 @@ __device__ __forceinline__ f32x4 mfma_pv(const uint2& a, const uint2& b, f32x4 c
     }
 }
 
-template <int D>
+// Cache element width: 2 bytes (fp16 / bf16, the compute dtype) or 1 byte
+// (OCP FP8 e4m3, converted to the compute dtype when staged).
+template <int D, bool FP8>
 struct TileRegs {
-    uint4 k[D / 32];
-    uint4 v[D / 32];
+    static constexpr int kBytes = FP8 ? 1 : 2; // bytes per cache element
+    static constexpr int L = D * kBytes / 16;  // lanes per token row (16 bytes each)
+    static constexpr int R = 64 / L;           // tokens per load instruction
+    static constexpr int NI = 16 / R;          // loads per tile and tensor
+    uint4 k[NI];
+    uint4 v[NI];
 };
 
 // Issue the K and V loads of the 16-token tile starting at t0 in row layout:
@@ -83,22 +89,24 @@ struct TileRegs {
 // (a prefetch past the end of the range) every lane loads the same 16 bytes at
 // the start of the caches instead: the loop then issues the same number of
 // loads on every path, which keeps the compiler's wait counts exact.
-template <int D, bool WIDE>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams& p, int win, int win_base, int t0,
-                                          int end, bool real, int lane, int kvh) {
-    constexpr int L = D / 8;
-    constexpr int R = 64 / L;
-    constexpr int NI = D / 32;
+template <int D, bool WIDE, bool FP8>
+__device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionParams& p, int win, int win_base,
+                                          int t0, int end, bool real, int lane, int kvh) {
+    using Regs = TileRegs<D, FP8>;
+    constexpr int EB = Regs::kBytes;
+    constexpr int L = Regs::L;
+    constexpr int R = Regs::R;
+    constexpr int NI = Regs::NI;
     const int rl = lane / L;
     const int pmask = (1 << p.page_shift) - 1;
-    const uint32_t col = static_cast<uint32_t>(kvh * D + 8 * (lane % L)) * 2u; // bytes within a token row
-    const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * 2u;            // bytes per token
+    const uint32_t col = static_cast<uint32_t>(kvh * D * EB + 16 * (lane % L)); // bytes within a token row
+    const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * EB;            // bytes per token
     if constexpr (WIDE) {
         // Wave-uniform page base (SGPRs) + 32-bit lane offsets: saddr-form loads.
         const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
         const int phys = __builtin_amdgcn_readlane(win, idx);
         const int64_t base =
-            real ? (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(t0 & pmask) * p.token_stride) * 2
+            real ? (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(t0 & pmask) * p.token_stride) * EB
                  : 0;
         const char* kb = reinterpret_cast<const char*>(p.k) + base;
         const char* vb = reinterpret_cast<const char*>(p.v) + base;
@@ -115,7 +123,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const PartitionParams&
             const int t = min(t0 + R * i + rl, end - 1);
             const int phys = __shfl(win, real ? (t >> p.page_shift) - win_base : 0, 64);
             const int64_t off =
-                real ? static_cast<int64_t>(phys) * p.page_stride * 2 + static_cast<int64_t>(t & pmask) * ts2 + col
+                real ? static_cast<int64_t>(phys) * p.page_stride * EB + static_cast<int64_t>(t & pmask) * ts2 + col
                      : 0;
             r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.k) + off));
             r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.v) + off));
@@ -137,18 +145,61 @@ struct VTile {
 
 // Part 1a of a tile: stage the K and V rows in the wave's LDS tiles.  After
 // this the tile's registers are free for the next prefetch.
-template <int D>
-__device__ __forceinline__ void stage_tile(const TileRegs<D>& r, uint16_t* lds, int lane) {
-    constexpr int L = D / 8;
-    constexpr int R = 64 / L;
-    constexpr int NI = D / 32;
+// Two FP8 e4m3 values (bytes 2w, 2w + 1 of x) to two 16-bit values of the
+// compute dtype, exactly (every e4m3 value is a bf16 and an fp16 value).
+template <bool BF16, bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_16(uint32_t x) {
+    if constexpr (BF16) {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, HI));
+    } else {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, HI));
+    }
+}
+
+// 16 FP8 values to 16 values of the compute dtype (two 16-byte chunks).
+template <bool BF16>
+__device__ __forceinline__ void fp8x16_to_16(const uint4& x, uint4& lo, uint4& hi) {
+    lo.x = fp8x2_to_16<BF16, false>(x.x);
+    lo.y = fp8x2_to_16<BF16, true>(x.x);
+    lo.z = fp8x2_to_16<BF16, false>(x.y);
+    lo.w = fp8x2_to_16<BF16, true>(x.y);
+    hi.x = fp8x2_to_16<BF16, false>(x.z);
+    hi.y = fp8x2_to_16<BF16, true>(x.z);
+    hi.z = fp8x2_to_16<BF16, false>(x.w);
+    hi.w = fp8x2_to_16<BF16, true>(x.w);
+}
+
+// Part 1a of a tile: stage the K and V rows in the wave's LDS tiles (FP8
+// rows converted to the compute dtype on the way).  After this the tile's
+// registers are free for the next prefetch.
+template <int D, bool FP8, bool BF16>
+__device__ __forceinline__ void stage_tile(const TileRegs<D, FP8>& r, uint16_t* lds, int lane) {
+    using Regs = TileRegs<D, FP8>;
+    constexpr int L = Regs::L;
+    constexpr int R = Regs::R;
+    constexpr int NI = Regs::NI;
     uint16_t* kt = lds;
     uint16_t* vt = lds + VTile<D>::kElems;
-    const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
+    if constexpr (FP8) {
+        const int wo = (lane / L) * VTile<D>::kRow + 16 * (lane % L);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
-        *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
+        for (int i = 0; i < NI; ++i) {
+            uint4 a;
+            uint4 b;
+            fp8x16_to_16<BF16>(r.k[i], a, b);
+            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = a;
+            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow + 8) = b;
+            fp8x16_to_16<BF16>(r.v[i], a, b);
+            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = a;
+            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow + 8) = b;
+        }
+    } else {
+        const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
+            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
+        }
     }
 }
 
@@ -184,6 +235,7 @@ struct MfmaMath {
     static constexpr int kHeads = 16 * NB;
     static constexpr int DT = D / 16;
     static constexpr bool kMultiQuery = MQ;
+    static constexpr bool kBF16 = BF16;
 
     // QK B operands: row 16 nb + n of the slice (n = lane & 15), dims
     // 8(4kk + j) .. +7 (zero past the slice).  MQ: per block, the lane's row
@@ -417,14 +469,15 @@ struct MfmaMath {
 
     // Output rows of the slice (bh_first + 16 nb + n with one query token, the
     // lane's rows with MQ): O / l rounded to 16 bits (RNE).
+    // out_scale multiplies the normalised rows (the V dequantisation scale).
     __device__ static void write_final(const PartitionParams& p, const Q& q, int64_t bh_first, int heads_here,
-                                       const Acc& a, int lane) {
+                                       const Acc& a, int lane, float out_scale) {
         const int j = lane >> 4;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int n = 16 * nb + (lane & 15);
             if (n < heads_here) {
-                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
+                const float inv = a.l[nb] > 0.f ? out_scale / a.l[nb] : 0.f;
                 int64_t row;
                 if constexpr (MQ) {
                     row = q.row[nb];
@@ -446,14 +499,14 @@ struct MfmaMath {
     // Partial of slice row h at index part_base + h * part_stride: O / l in
     // fp32 and the log2-domain LSE m + log2(l).
     __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
-                                         int heads_here, const Acc& a, int lane) {
+                                         int heads_here, const Acc& a, int lane, float out_scale) {
         const int j = lane >> 4;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int n = 16 * nb + (lane & 15);
             if (n < heads_here) {
                 const int64_t pi = part_base + n * part_stride;
-                const float inv = a.l[nb] > 0.f ? 1.f / a.l[nb] : 0.f;
+                const float inv = a.l[nb] > 0.f ? out_scale / a.l[nb] : 0.f;
                 float* dst = p.part_o + pi * D + 4 * j;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
@@ -534,6 +587,7 @@ struct ValuMath {
     static constexpr int kHeads = NH;
     static constexpr int E = D / 64; // output dims per lane and head
     static constexpr bool kMultiQuery = false; // one query token, no mask
+    static constexpr bool kBF16 = BF16;
 
     // Lane (t, c) = (lane & 15, lane >> 4): q of every head, dims 8(4i + c) .. +7.
     struct Q {
@@ -652,11 +706,11 @@ struct ValuMath {
     }
 
     __device__ static void write_final(const PartitionParams& p, const Q&, int64_t bh_first, int heads_here,
-                                       const Acc& a, int lane) {
+                                       const Acc& a, int lane, float out_scale) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             if (h < heads_here) {
-                const float inv = a.l[h] > 0.f ? 1.f / a.l[h] : 0.f;
+                const float inv = a.l[h] > 0.f ? out_scale / a.l[h] : 0.f;
                 uint16_t* dst = p.out + (bh_first + h) * D + E * lane;
                 if constexpr (E == 1) {
                     dst[0] = from_f32<BF16>(a.o[h][0] * inv);
@@ -673,12 +727,12 @@ struct ValuMath {
     }
 
     __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
-                                         int heads_here, const Acc& a, int lane) {
+                                         int heads_here, const Acc& a, int lane, float out_scale) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
             if (h < heads_here) {
                 const int64_t pi = part_base + h * part_stride;
-                const float inv = a.l[h] > 0.f ? 1.f / a.l[h] : 0.f;
+                const float inv = a.l[h] > 0.f ? out_scale / a.l[h] : 0.f;
                 float* dst = p.part_o + pi * D + E * lane;
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
@@ -739,11 +793,11 @@ struct ValuMath {
 // adds the page-window refresh for ranges longer than 64 pages (a dependent
 // global load, so it drains the pipeline once per 64 pages); the common path
 // has none and every prefetch is unconditional, so all waits are exact.
-template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD>
+template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD, bool FP8>
 __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_t* __restrict__ bt_row, int last_page,
                                           int& win, int& win_base, const typename Math::Q& q,
                                           typename Math::Acc& acc, uint16_t* lds, int t, int end, int lane,
-                                          int kvh) {
+                                          int kvh, float scale_log2) {
     auto ensure_window = [&](int tn) {
         if constexpr (RELOAD) {
             const int tl = min(tn + 15, end - 1);
@@ -760,38 +814,38 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
     // Per tile: stage the landed tile in LDS, immediately issue the prefetch
     // into the freed registers (pinned there by a scheduling barrier), then
     // compute.  The prefetch is in flight for the whole QK / softmax / PV.
-    TileRegs<D> ra;
-    load_tile<D, WIDE>(ra, p, win, win_base, t, end, true, lane, kvh);
+    TileRegs<D, FP8> ra;
+    load_tile<D, WIDE, FP8>(ra, p, win, win_base, t, end, true, lane, kvh);
     if constexpr (DEPTH == 1) {
         for (int k = 0; k < ntiles; ++k) {
-            stage_tile<D>(ra, lds, lane);
+            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
             ensure_window(t + 16);
-            load_tile<D, WIDE>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
+            load_tile<D, WIDE, FP8>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
             __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
+            Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
         }
     } else {
-        TileRegs<D> rb;
+        TileRegs<D, FP8> rb;
         ensure_window(t + 16);
-        load_tile<D, WIDE>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
+        load_tile<D, WIDE, FP8>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
         for (int k = 0; k + 2 <= ntiles; k += 2) {
-            stage_tile<D>(ra, lds, lane);
+            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
             ensure_window(t + 32);
-            load_tile<D, WIDE>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
+            load_tile<D, WIDE, FP8>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
             __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
+            Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
-            stage_tile<D>(rb, lds, lane);
+            stage_tile<D, FP8, Math::kBF16>(rb, lds, lane);
             ensure_window(t + 32);
-            load_tile<D, WIDE>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
+            load_tile<D, WIDE, FP8>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
             __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
+            Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
         }
         if (ntiles & 1) {
-            stage_tile<D>(ra, lds, lane);
-            Math::tile(q, acc, lds, t, end, lane, p.scale_log2);
+            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
+            Math::tile(q, acc, lds, t, end, lane, scale_log2);
         }
     }
 }
@@ -799,26 +853,47 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 // Attention of one head slice over tokens [begin, end) (begin < end), the page
 // window already loaded at win_base = begin / P.  Leaves Math's accumulator
 // (unnormalised O, reference max, denominator) finished.
-template <typename Math, int D, bool WIDE, int DEPTH>
+template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
 __device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
                                              int win_base, const typename Math::Q& q, uint16_t* lds, int begin,
-                                             int end, int lane, int kvh, typename Math::Acc& acc) {
+                                             int end, int lane, int kvh, typename Math::Acc& acc, float scale_log2) {
     Math::init(acc);
     const int last_page = (end - 1) >> p.page_shift;
     if (last_page - win_base < 64) {
         // Common case: the whole range fits in one page window.
-        tile_loop<Math, D, WIDE, DEPTH, false>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end, lane,
-                                               kvh);
+        tile_loop<Math, D, WIDE, DEPTH, false, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
+                                                    lane, kvh, scale_log2);
     } else {
-        tile_loop<Math, D, WIDE, DEPTH, true>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end, lane,
-                                              kvh);
+        tile_loop<Math, D, WIDE, DEPTH, true, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
+                                                   lane, kvh, scale_log2);
     }
     Math::finish(acc);
 }
 
+// Per-KV-head dequantisation of FP8 caches: the K scale folds into the softmax
+// scale (q . (s k) = s (q . k)), the V scale into the normalised output.
+struct KvScales {
+    float score_log2; // softmax_scale * log2(e) * k_scale
+    float out;        // v_scale
+};
+
+template <bool FP8>
+__device__ __forceinline__ KvScales kv_scales(const PartitionParams& p, int kvh) {
+    KvScales s{p.scale_log2, 1.f};
+    if constexpr (FP8) {
+        if (p.k_scale != nullptr) {
+            s.score_log2 *= p.k_scale[kvh];
+        }
+        if (p.v_scale != nullptr) {
+            s.out = p.v_scale[kvh];
+        }
+    }
+    return s;
+}
+
 // Split schedules (one split, page-balanced splits, token windows): one wave
 // per work item (b, kv head, head group, split).
-template <typename Math, int D, bool WIDE, int DEPTH>
+template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
 __global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
 void partition_split_kernel(PartitionParams p) {
     constexpr int kWaves = kWavesPerGroup;
@@ -885,13 +960,14 @@ void partition_split_kernel(PartitionParams p) {
         win = load_page_window(bt_row, win_base, (range.end - 1) >> p.page_shift, lane, p.num_pages);
     }
 
+    const KvScales ks = kv_scales<FP8>(p, kvh);
     typename Math::Acc acc;
-    attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], range.begin, range.end, lane,
-                                       kvh, acc);
+    attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds_tiles[wave], range.begin, range.end,
+                                            lane, kvh, acc, ks.score_log2);
     if (p.splits == 1) {
-        Math::write_final(p, q, bh_first, heads_here, acc, lane);
+        Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
     } else {
-        Math::write_partial(p, sr_first * p.splits + split, p.splits, heads_here, acc, lane);
+        Math::write_partial(p, sr_first * p.splits + split, p.splits, heads_here, acc, lane, ks.out);
     }
 }
 
@@ -900,7 +976,7 @@ void partition_split_kernel(PartitionParams p) {
 // then parks its finished accumulator in its own LDS tile and wave 0 merges
 // the four (online-softmax merge) and writes the item's output or partial.
 // Still one pass per item and no workspace: only the latency changes.
-template <typename Math, int D, bool WIDE, int DEPTH>
+template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
 __global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
 void partition_item_group_kernel(PartitionParams p) {
     constexpr int kWaves = kWavesPerGroup;
@@ -941,12 +1017,13 @@ void partition_item_group_kernel(PartitionParams p) {
     const int sub_begin = range.begin + 16 * min(ntiles, wave * per);
     const int sub_end = min(range.end, range.begin + 16 * min(ntiles, (wave + 1) * per));
 
+    const KvScales ks = kv_scales<FP8>(p, it.kvh);
     typename Math::Acc acc;
     if (sub_begin < sub_end) {
         const int win_base = sub_begin >> p.page_shift;
         const int win = load_page_window(bt_row, win_base, (sub_end - 1) >> p.page_shift, lane, p.num_pages);
-        attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds_tiles[wave], sub_begin, sub_end, lane,
-                                           it.kvh, acc);
+        attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds_tiles[wave], sub_begin, sub_end,
+                                                lane, it.kvh, acc, ks.score_log2);
     } else {
         Math::init(acc);
         Math::finish(acc);
@@ -963,9 +1040,9 @@ void partition_item_group_kernel(PartitionParams p) {
         Math::merge(acc, other);
     }
     if (p.splits == 1) {
-        Math::write_final(p, q, bh_first, heads_here, acc, lane);
+        Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
     } else {
-        Math::write_partial(p, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane);
+        Math::write_partial(p, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane, ks.out);
     }
 }
 
@@ -975,7 +1052,7 @@ void partition_item_group_kernel(PartitionParams p) {
 // output; any other leaves a partial in slot w + r for the combine.  The workgroup's LDS request is padded on the
 // host so that one workgroup occupies a CU: the dispatcher then spreads the
 // grid over all CUs instead of doubling some up while others idle.
-template <typename Math, int D, bool WIDE, int DEPTH, int WAVES>
+template <typename Math, int D, bool WIDE, int DEPTH, int WAVES, bool FP8>
 __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[WAVES][2 * VTile<D>::kElems];
 
@@ -1026,13 +1103,15 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 const int win_base = begin >> p.page_shift;
                 const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
+                const KvScales ks = kv_scales<FP8>(p, kvh);
                 typename Math::Acc acc;
-                attend_range<Math, D, WIDE, DEPTH>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc);
+                attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc,
+                                                        ks.score_log2);
                 if (t_lo == 0 && t_hi == nb) {
-                    Math::write_final(p, q, bh_first, heads_here, acc, lane);
+                    Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
                 } else {
                     const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
-                    Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane);
+                    Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane, ks.out);
                 }
             }
             vs += units;
@@ -1065,7 +1144,16 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
 #endif
 constexpr int kSplitDepthFewItems = 2;
 
-template <typename Math, int D, bool WIDE>
+// FP8 tiles are half the bytes: two of them in flight keep as many bytes
+// loading as one 16-bit tile.  Measured on MI355X (C2 / C3 / C4 / C5 with FP8
+// caches): 40.1 / 164 / 187 / 112 us with one tile, 32.6 / 129 / 134 / 111 us
+// with two; eight waves per CU instead of four gave 32.9 / 132 / 140 / 118.
+template <bool FP8>
+constexpr int kv_depth() {
+    return FP8 ? 2 : PKV_MFMA_DEPTH;
+}
+
+template <typename Math, int D, bool WIDE, bool FP8>
 static void launch_tiles(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = kTileWaves;
     const int blocks = (p.tile_workers + kWaves - 1) / kWaves;
@@ -1074,36 +1162,50 @@ static void launch_tiles(const PartitionParams& p, hipStream_t stream, const Lau
     constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
     constexpr size_t kHalf = 80 * 1024;
     const size_t dyn = kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
-    launch_kernel(partition_tiles_kernel<Math, D, WIDE, PKV_MFMA_DEPTH, kWaves>, dim3(blocks), dim3(64 * kWaves), dyn,
-                  stream, ev, p);
+    launch_kernel(partition_tiles_kernel<Math, D, WIDE, kv_depth<FP8>(), kWaves, FP8>, dim3(blocks),
+                  dim3(64 * kWaves), dyn, stream, ev, p);
 }
 
-template <typename Math, int D, bool WIDE>
+template <typename Math, int D, bool WIDE, bool FP8>
 static void launch_split(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     const dim3 block(64 * kWavesPerGroup);
     if (p.num_items < kComputeUnits) {
         // Fewer items than CUs: a workgroup per item, latency-bound, two tiles in flight.
-        launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems>, dim3(p.num_items), block, 0,
-                      stream, ev, p);
+        launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems, FP8>, dim3(p.num_items), block,
+                      0, stream, ev, p);
     } else {
-        launch_kernel(partition_split_kernel<Math, D, WIDE, PKV_MFMA_DEPTH>, dim3(p.num_groups), block, 0, stream,
-                      ev, p);
+        launch_kernel(partition_split_kernel<Math, D, WIDE, kv_depth<FP8>(), FP8>, dim3(p.num_groups), block, 0,
+                      stream, ev, p);
     }
 }
 
-template <typename Math, int D>
-static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
+template <typename Math, int D, bool FP8>
+static void launch_math_kv(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     const bool wide = p.page_shift >= 4;
     if (p.tile_workers > 0) {
         if (wide) {
-            launch_tiles<Math, D, true>(p, stream, ev);
+            launch_tiles<Math, D, true, FP8>(p, stream, ev);
         } else {
-            launch_tiles<Math, D, false>(p, stream, ev);
+            launch_tiles<Math, D, false, FP8>(p, stream, ev);
         }
     } else if (wide) {
-        launch_split<Math, D, true>(p, stream, ev);
+        launch_split<Math, D, true, FP8>(p, stream, ev);
     } else {
-        launch_split<Math, D, false>(p, stream, ev);
+        launch_split<Math, D, false, FP8>(p, stream, ev);
+    }
+}
+
+// FP8 caches only with the MFMA policies.
+template <typename Math, int D>
+static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
+    if (p.kv_fp8) {
+        if constexpr (Math::kHeads >= 16) {
+            launch_math_kv<Math, D, true>(p, stream, ev);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else {
+        launch_math_kv<Math, D, false>(p, stream, ev);
     }
     return hipGetLastError();
 }

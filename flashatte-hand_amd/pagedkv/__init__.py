@@ -31,6 +31,8 @@ from ._lib import (  # noqa: F401  (re-exported constants)
     PKV_ELAUNCH,
     PKV_ENOWORKSPACE,
     PKV_EUNSUPPORTED,
+    PKV_KV_DTYPE_FP8_E4M3,
+    PKV_KV_DTYPE_SAME,
     PKV_MASK_CAUSAL,
     PKV_MASK_WINDOW,
     PKV_MAX_SPLITS,
@@ -98,6 +100,9 @@ def make_desc(
     window_size=(-1, -1),
     alibi_slopes: int = 0,
     alibi_batch_stride: int = 0,
+    kv_dtype: int = PKV_KV_DTYPE_SAME,
+    k_scale: int = 0,
+    v_scale: int = 0,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -119,10 +124,33 @@ def make_desc(
     window_size = tuple(window_size)
     d.mask = (PKV_MASK_CAUSAL if causal else 0) | (PKV_MASK_WINDOW if window_size != (-1, -1) else 0)
     d.window_left, d.window_right = window_size
-    d.reserved2 = 0
+    d.kv_dtype = kv_dtype
     d.alibi_slopes = alibi_slopes or None
     d.alibi_batch_stride = alibi_batch_stride
+    d.k_scale = k_scale or None
+    d.v_scale = v_scale or None
     return d
+
+
+def _kv_dtype(cache, q_dtype) -> int:
+    """Element type code of a cache tensor: the 16-bit dtype of q, or OCP FP8 e4m3."""
+    torch = _torch()
+    if cache.dtype == torch.float8_e4m3fn:
+        return PKV_KV_DTYPE_FP8_E4M3
+    if cache.dtype != q_dtype:
+        raise PkvError(PKV_EINVAL, "caches must have q's dtype or be torch.float8_e4m3fn")
+    return PKV_KV_DTYPE_SAME
+
+
+def _scale_ptr(name, scale, Hk) -> int:
+    """Device pointer of an optional fp32 [Hk] per-KV-head scale."""
+    torch = _torch()
+    if scale is None:
+        return 0
+    _check_cuda(name, scale)
+    if scale.dtype != torch.float32 or tuple(scale.shape) != (Hk,):
+        raise PkvError(PKV_EINVAL, f"{name} must be fp32 [num_heads_k]")
+    return scale.data_ptr()
 
 
 def workspace_size(desc: PkvDecodeDesc, num_splits: int = 0) -> int:
@@ -173,8 +201,14 @@ def decode(
     causal: bool = False,
     window_size=(-1, -1),
     alibi_slopes=None,
+    k_scale=None,
+    v_scale=None,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
+
+    Caches of dtype ``torch.float8_e4m3fn`` are OCP FP8 e4m3 with optional fp32
+    per-KV-head dequantisation scales ``k_scale`` / ``v_scale`` ([Hk]); the
+    appended tokens are then quantised with the same scales.
 
     ``q`` is ``[B, M, H, D]``: M > 1 query tokens per row (speculative-decode
     verify) sit at the last M positions of each row; ``causal``,
@@ -198,8 +232,9 @@ def decode(
         raise PkvError(PKV_EINVAL, "k_cache / v_cache must both be [num_pages, P, Hk, D]")
     if block_table.dtype != torch.int32 or cache_seqlens.dtype != torch.int32:
         raise PkvError(PKV_EINVAL, "block_table and cache_seqlens must be int32")
-    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
-        raise PkvError(PKV_EINVAL, "q, k_cache and v_cache must share a dtype")
+    if k_cache.dtype != v_cache.dtype:
+        raise PkvError(PKV_EINVAL, "k_cache and v_cache must share a dtype")
+    kv_dtype = _kv_dtype(k_cache, q.dtype)
     B, M, H, D = q.shape
     num_pages, P, Hk, Dk = k_cache.shape
     if Dk != D or block_table.dim() != 2 or block_table.shape[0] != B or cache_seqlens.numel() != B:
@@ -222,11 +257,14 @@ def decode(
     seqlen_new = 0
     if k_new is not None or v_new is not None:
         seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
+        if k_new.dtype != q.dtype:
+            raise PkvError(PKV_EINVAL, "k / v must have q's dtype")
     desc = make_desc(
         batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
         block_table_stride=block_table.shape[1], dtype=_dtype_code(q.dtype), max_seqlen=max_seqlen, path=path,
         split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
-        alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride,
+        alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride, kv_dtype=kv_dtype,
+        k_scale=_scale_ptr("k_scale", k_scale, Hk), v_scale=_scale_ptr("v_scale", v_scale, Hk),
     )
     lib = _lib.load()
     if seqlen_new:
@@ -264,15 +302,19 @@ def _check_new_tokens(k_new, v_new, k_cache, batch: int) -> int:
         raise PkvError(PKV_EINVAL, "k and v must be given together")
     _check_cuda("k", k_new)
     _check_cuda("v", v_new)
+    torch = _torch()
     _, _, Hk, D = k_cache.shape
     if k_new.dim() != 4 or k_new.shape != v_new.shape or k_new.shape[0] != batch or tuple(k_new.shape[2:]) != (Hk, D):
         raise PkvError(PKV_EINVAL, "k / v must both be [B, seqlen_new, Hk, D]")
-    if k_new.dtype != k_cache.dtype or v_new.dtype != k_cache.dtype:
+    if k_new.dtype != v_new.dtype or k_new.dtype not in (torch.float16, torch.bfloat16):
+        raise PkvError(PKV_EINVAL, "k / v must be fp16 or bf16")
+    if k_cache.dtype != torch.float8_e4m3fn and k_new.dtype != k_cache.dtype:
         raise PkvError(PKV_EINVAL, "k / v must have the caches' dtype")
     return int(k_new.shape[1])
 
 
-def append_kv(k_new, v_new, k_cache, v_cache, block_table, cache_seqlens, *, stream=None) -> None:
+def append_kv(k_new, v_new, k_cache, v_cache, block_table, cache_seqlens, *, k_scale=None, v_scale=None,
+              stream=None) -> None:
     """Write ``k_new`` / ``v_new`` ([B, seqlen_new, Hk, D]) into the paged caches in place.
 
     Token j of row b lands at position ``max(cache_seqlens[b], 0) + j`` of the
@@ -295,7 +337,9 @@ def append_kv(k_new, v_new, k_cache, v_cache, block_table, cache_seqlens, *, str
     seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
     num_pages, P, Hk, D = k_cache.shape
     desc = make_desc(batch=B, num_heads=Hk, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
-                     block_table_stride=block_table.shape[1], dtype=_dtype_code(k_cache.dtype))
+                     block_table_stride=block_table.shape[1], dtype=_dtype_code(k_new.dtype),
+                     kv_dtype=_kv_dtype(k_cache, k_new.dtype), k_scale=_scale_ptr("k_scale", k_scale, Hk),
+                     v_scale=_scale_ptr("v_scale", v_scale, Hk))
     if stream is None:
         stream = torch.cuda.current_stream(k_cache.device).cuda_stream
     st = _lib.load().pkv_append_kv(
@@ -306,7 +350,8 @@ def append_kv(k_new, v_new, k_cache, v_cache, block_table, cache_seqlens, *, str
         raise PkvError(st, "pkv_append_kv")
 
 
-def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *, stream=None) -> None:
+def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *, k_scale=None, v_scale=None,
+                            stream=None) -> None:
     """Write token rows ``key`` / ``value`` ([num_tokens, Hk, D]) to flat cache slots in place.
 
     ``slot_mapping[i] = page * P + slot`` (int64); a negative slot is padding and
@@ -322,12 +367,14 @@ def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *,
     num_pages, P, Hk, D = key_cache.shape
     if key.dim() != 3 or key.shape != value.shape or tuple(key.shape[1:]) != (Hk, D):
         raise PkvError(PKV_EINVAL, "key / value must both be [num_tokens, Hk, D]")
-    if key.dtype != key_cache.dtype or value.dtype != key_cache.dtype:
-        raise PkvError(PKV_EINVAL, "key / value must have the caches' dtype")
+    if key.dtype != value.dtype or key.dtype not in (torch.float16, torch.bfloat16):
+        raise PkvError(PKV_EINVAL, "key / value must be fp16 or bf16")
     if slot_mapping.dtype != torch.int64 or slot_mapping.numel() != key.shape[0]:
         raise PkvError(PKV_EINVAL, "slot_mapping must be int64 with one entry per token")
     desc = make_desc(batch=0, num_heads=0, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
-                     block_table_stride=0, dtype=_dtype_code(key_cache.dtype))
+                     block_table_stride=0, dtype=_dtype_code(key.dtype),
+                     kv_dtype=_kv_dtype(key_cache, key.dtype), k_scale=_scale_ptr("k_scale", k_scale, Hk),
+                     v_scale=_scale_ptr("v_scale", v_scale, Hk))
     if stream is None:
         stream = torch.cuda.current_stream(key_cache.device).cuda_stream
     st = _lib.load().pkv_reshape_and_cache(

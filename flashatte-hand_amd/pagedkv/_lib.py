@@ -21,6 +21,9 @@ PKV_ELAUNCH = 4
 PKV_DTYPE_F16 = 0
 PKV_DTYPE_BF16 = 1
 
+PKV_KV_DTYPE_SAME = 0
+PKV_KV_DTYPE_FP8_E4M3 = 1
+
 PKV_PATH_AUTO = 0
 PKV_PATH_VALU = 1
 PKV_PATH_MFMA = 2
@@ -76,9 +79,11 @@ class PkvDecodeDesc(ctypes.Structure):
         ("mask", ctypes.c_int32),
         ("window_left", ctypes.c_int32),
         ("window_right", ctypes.c_int32),
-        ("reserved2", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
         ("alibi_slopes", ctypes.c_void_p),
         ("alibi_batch_stride", ctypes.c_int64),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
     ]
 
 

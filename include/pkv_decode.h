@@ -8,9 +8,9 @@
  *
  * Tensor layouts (identical to the reference's flash-attn layout,
  * scripts/evaluate_flashattn_submission.py:127-143, 249):
- *   q, out         [B, 1, H, D]           16-bit (fp16 or bf16), contiguous
+ *   q, out         [B, M, H, D]           16-bit (fp16 or bf16), contiguous (M = seqlen_q, 1 for decode)
  *   k_cache,
- *   v_cache        [num_pages, P, Hk, D]  16-bit, contiguous
+ *   v_cache        [num_pages, P, Hk, D]  16-bit like q, or OCP FP8 e4m3 bytes (kv_dtype), contiguous
  *   block_table    [B, block_table_stride] int32 physical page ids
  *   cache_seqlens  [B]                    int32 valid tokens per row
  * Token t of row b lives in page block_table[b][t / P], slot t % P; only
@@ -37,6 +37,11 @@ extern "C" {
 
 #define PKV_DTYPE_F16 0
 #define PKV_DTYPE_BF16 1
+
+/* Element type of k_cache / v_cache (pkv_decode_desc.kv_dtype). */
+#define PKV_KV_DTYPE_SAME 0     /* desc->dtype, like q and out */
+#define PKV_KV_DTYPE_FP8_E4M3 1 /* OCP FP8 e4m3 (1 byte; finite range +-448, no infinities), dequantised as
+                                   value * k_scale / v_scale of the KV head; needs the MFMA path */
 
 /* Kernel family selector (pkv_decode_desc.path). */
 #define PKV_PATH_AUTO 0        /* measured choice per shape */
@@ -88,9 +93,12 @@ typedef struct pkv_decode_desc {
     int32_t window_left;        /* PKV_MASK_WINDOW: keys j >= pos - window_left (-1 = unbounded) */
     int32_t window_right;       /* PKV_MASK_WINDOW: keys j <= pos + window_right (-1 = unbounded);
                                    PKV_MASK_CAUSAL forces 0 */
-    int32_t reserved2;          /* must be 0 */
+    int32_t kv_dtype;           /* PKV_KV_DTYPE_*: element type of k_cache / v_cache */
     const float* alibi_slopes;  /* optional fp32 [H] or [B, H]: score -= slope * |pos - j| */
     int64_t alibi_batch_stride; /* 0 for [H] slopes, H for [B, H] */
+    const float* k_scale;       /* FP8 caches: optional fp32 [Hk] device array, K = fp8 * k_scale[kv head];
+                                   NULL = 1.  The append divides by it before rounding to FP8. */
+    const float* v_scale;       /* FP8 caches: the same for V */
 } pkv_decode_desc;
 
 /*
@@ -156,6 +164,9 @@ int pkv_decode_path(const pkv_decode_desc* desc);
  * token j of row b at position max(cache_seqlens[b], 0) + j, i.e. slot
  * (pos % P) of page block_table[b][pos / P].
  *   k_new, v_new  [B, seqlen_new, Hk, D]  16-bit (desc->dtype), contiguous, 16-byte aligned
+ * FP8 caches (desc->kv_dtype): each value x is stored as the e4m3 value
+ * nearest to x * (1 / scale) (fp32 arithmetic, ties to even), saturated to
+ * +-448; the scale is the KV head's k_scale / v_scale (1 when NULL).
  * desc is the attention calls' descriptor (it must pass the same checks);
  * the append uses its batch, num_heads_k, head_dim, page_size, num_pages,
  * block_table_stride and dtype, and ignores the workspace.  Positions at or past

@@ -21,6 +21,9 @@
  *                              position i + L - M; causal keeps keys j <= pos; a window keeps
  *                              pos - left <= j <= pos + right; ALiBi adds -slope * |pos - j|
  *                              to the scaled score; a query with no visible key gives 0
+ *   pkv_oracle_attn8_f64       the same over OCP FP8 e4m3 caches with per-KV-head scales (no
+ *                              counterpart in the reference, which keeps 16-bit caches)
+ *   pkv_oracle_e4m3_to_f32     the OCP 8-bit floating point specification's E4M3 encoding
  *
  * How each is pinned (tests/test_oracle.py): the dense fp64 result against an
  * independent numpy formula (including the reference's diagnostic seeds),
@@ -353,13 +356,41 @@ void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const ui
     }
 }
 
+/* ---------------------------------------------------------------- OCP FP8 e4m3 */
+
+/* e4m3 (OCP "E4M3FN"): sign, 4 exponent bits (bias 7), 3 mantissa bits; no
+ * infinities, S.1111.111 is NaN, max finite 448; exponent 0 is subnormal
+ * (m / 8 * 2^-6). */
+float pkv_oracle_e4m3_to_f32(uint8_t b) {
+    const int sign = b >> 7;
+    const int e = (b >> 3) & 15;
+    const int m = b & 7;
+    float v;
+    if (e == 15 && m == 7) {
+        v = NAN;
+    } else if (e == 0) {
+        v = ldexpf((float)m / 8.0f, -6);
+    } else {
+        v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    }
+    return sign ? -v : v;
+}
+
 /* ---------------------------------------------------------------- fp64 dense, several queries, masks */
 
-void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
-                         const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
-                         int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
-                         const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out) {
+/* Cache element t (16-bit of dtype dt, or e4m3 byte times scale) as double. */
+static inline double kv_elem(const void* cache, int64_t idx, int32_t dt, int kv_fp8, double scale) {
+    if (kv_fp8) {
+        return (double)pkv_oracle_e4m3_to_f32(((const uint8_t*)cache)[idx]) * scale;
+    }
+    return (double)to_f32(((const uint16_t*)cache)[idx], dt);
+}
+
+static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const void* k_cache, const void* v_cache,
+                          const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_q, int causal,
+                          int64_t window_left, int64_t window_right, const float* alibi_slopes,
+                          int64_t alibi_batch_stride, int kv_fp8, const float* k_scale, const float* v_scale,
+                          double softmax_scale, double* out) {
     build_f16_table();
     set_threads(d);
     const int64_t B = d->batch, H = d->num_heads, D = d->head_dim, M = seqlen_q;
@@ -386,6 +417,8 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
             const int64_t n = row_seqlen(d, cache_seqlens, b);
             const int64_t pos = i + n - M;
             const double slope = alibi_slopes ? (double)alibi_slopes[b * alibi_batch_stride + h] : 0.0;
+            const double ks = (kv_fp8 && k_scale) ? (double)k_scale[kvh] : 1.0;
+            const double vs = (kv_fp8 && v_scale) ? (double)v_scale[kvh] : 1.0;
             double* o = out + row * D;
             for (int64_t c = 0; c < D; ++c) {
                 o[c] = 0.0;
@@ -410,10 +443,10 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                     scores[t] = -INFINITY;
                     continue;
                 }
-                const uint16_t* krow = k_cache + token_offset(d, block_table, b, t, kvh);
+                const int64_t koff = token_offset(d, block_table, b, t, kvh);
                 double s = 0.0;
                 for (int64_t c = 0; c < D; ++c) {
-                    s += qd[c] * (double)to_f32(krow[c], dt);
+                    s += qd[c] * kv_elem(k_cache, koff + c, dt, kv_fp8, ks);
                 }
                 scores[t] = s * softmax_scale - slope * fabs((double)(pos - t));
                 if (scores[t] > mx) {
@@ -430,9 +463,9 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                 }
                 const double p = exp(scores[t] - mx);
                 denom += p;
-                const uint16_t* vrow = v_cache + token_offset(d, block_table, b, t, kvh);
+                const int64_t voff = token_offset(d, block_table, b, t, kvh);
                 for (int64_t c = 0; c < D; ++c) {
-                    acc[c] += p * (double)to_f32(vrow[c], dt);
+                    acc[c] += p * kv_elem(v_cache, voff + c, dt, kv_fp8, vs);
                 }
             }
             for (int64_t c = 0; c < D; ++c) {
@@ -442,6 +475,24 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
         free(scores);
         free(qd);
     }
+}
+
+void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
+                         const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
+                         int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
+                         const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
+                         double* out) {
+    attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
+                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out);
+}
+
+void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint8_t* k_cache,
+                          const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
+                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
+                          const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
+                          const float* v_scale, double softmax_scale, double* out) {
+    attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
+                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out);
 }
 
 /* ---------------------------------------------------------------- split-KV algebra */

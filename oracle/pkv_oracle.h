@@ -67,6 +67,17 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
                          double* out);
 
+/* OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 = NaN, max 448) to fp32. */
+float pkv_oracle_e4m3_to_f32(uint8_t b);
+
+/* pkv_oracle_attn_f64 over FP8 e4m3 caches: element x of KV head kvh stands
+ * for e4m3(x) * k_scale[kvh] (v_scale for V; NULL scales = 1). */
+void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint8_t* k_cache,
+                          const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
+                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
+                          const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
+                          const float* v_scale, double softmax_scale, double* out);
+
 /* Split-KV partition step (best_flashattn_kvcache_decode.cu:664-697, 782-864):
  * split s of row b covers pages [n*s/S, n*(s+1)/S) of its n valid pages;
  * exp2-domain fp32 online softmax; part_o [B*H*S, D] normalised, part_lse

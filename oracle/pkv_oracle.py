@@ -72,6 +72,13 @@ def load():
                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                         ctypes.c_double, _f64p]
     lib.pkv_oracle_attn_f64.restype = None
+    _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+    lib.pkv_oracle_attn8_f64.argtypes = [dp, _u16p, _u8p, _u8p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
+                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double, _f64p]
+    lib.pkv_oracle_attn8_f64.restype = None
+    lib.pkv_oracle_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+    lib.pkv_oracle_e4m3_to_f32.restype = ctypes.c_float
     for n in ("pkv_oracle_f16_to_f32", "pkv_oracle_bf16_to_f32"):
         getattr(lib, n).argtypes = [ctypes.c_uint16]
         getattr(lib, n).restype = ctypes.c_float
@@ -141,6 +148,33 @@ def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=Fal
                             int(window[0]), int(window[1]),
                             None if slopes is None else slopes.ctypes.data_as(ctypes.c_void_p), int(stride),
                             float(scale), out)
+    return out
+
+
+def attn8_f64(q, k_cache8, v_cache8, block_table, seqlens, scale, dtype, k_scale=None, v_scale=None, causal=False,
+              window=(-1, -1), alibi=None, threads=0):
+    """attn_f64 over OCP FP8 e4m3 caches (uint8 [num_pages, P, Hk, D]) with per-KV-head fp32 scales."""
+    lib = load()
+    B, M, H, D = q.shape
+    num_pages, P, Hk, _ = k_cache8.shape
+    d = dims(B, H, Hk, D, P, num_pages, block_table.shape[1], dtype, threads)
+    out = np.empty(q.shape, dtype=np.float64)
+    keep = []
+
+    def ptr(a):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        keep.append(a)
+        return a.ctypes.data_as(ctypes.c_void_p)
+
+    stride = 0
+    if alibi is not None:
+        stride = H if np.ndim(alibi) == 2 else 0
+    lib.pkv_oracle_attn8_f64(ctypes.byref(d), _c(q, np.uint16), _c(k_cache8, np.uint8), _c(v_cache8, np.uint8),
+                             _c(block_table, np.int32), _c(seqlens, np.int32), int(M), int(bool(causal)),
+                             int(window[0]), int(window[1]), ptr(alibi), int(stride), ptr(k_scale), ptr(v_scale),
+                             float(scale), out)
     return out
 
 
@@ -246,3 +280,50 @@ def reshape_and_cache(k_cache, v_cache, key, value, slot_mapping, inplace=False)
 def appended_seqlens(seqlens, seqlen_new):
     """Row lengths the attention covers after an append of seqlen_new tokens."""
     return (np.maximum(np.asarray(seqlens, dtype=np.int64), 0) + seqlen_new).astype(np.int32)
+
+
+
+# ------------------------------------------------------------------ OCP FP8 e4m3 (numpy)
+#
+# The OCP 8-bit floating point specification's E4M3 ("e4m3fn"): bias 7, 3
+# mantissa bits, no infinities, S.1111.111 is NaN, largest finite 448.
+# Quantisation (the append into FP8 caches): y = x * (1 / scale) in fp32,
+# saturated to +-448, rounded to the nearest e4m3 value, ties to even.
+
+def e4m3_to_f32(b):
+    """Values of e4m3 bytes (uint8 array) as float32, from the format definition."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int32)
+    sign = np.where(b >> 7, -1.0, 1.0)
+    e = (b >> 3) & 15
+    m = b & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    out = (sign * mag).astype(np.float32)
+    out[(e == 15) & (m == 7)] = np.nan
+    return out
+
+
+_E4M3_POS = e4m3_to_f32(np.arange(0x7F, dtype=np.uint8))  # codes 0x00..0x7e: 0 .. 448, increasing
+
+
+def f32_to_e4m3(x):
+    """Nearest e4m3 byte to each float32 (ties to the even code), saturated to +-448; NaN -> 0x7f."""
+    x = np.asarray(x, dtype=np.float32)
+    mag = np.minimum(np.abs(x), np.float32(448.0)).astype(np.float64)
+    hi = np.clip(np.searchsorted(_E4M3_POS, mag, side="left"), 0, 0x7E)
+    lo = np.maximum(hi - 1, 0)
+    d_lo = mag - _E4M3_POS[lo]
+    d_hi = _E4M3_POS[hi] - mag
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    code = code | np.where(np.signbit(x), 0x80, 0).astype(np.uint8)
+    code[np.isnan(x)] = 0x7F
+    return code
+
+
+def quantize_e4m3(bits, dtype, scale=None):
+    """16-bit rows [..., Hk, D] (uint16 bits of dtype) to e4m3 bytes with per-KV-head scales [Hk]."""
+    x = bits_to_f32(bits, dtype)
+    if scale is not None:
+        inv = (np.float32(1.0) / np.asarray(scale, dtype=np.float32)).astype(np.float32)
+        x = (x * inv[:, None]).astype(np.float32)
+    return f32_to_e4m3(x)

@@ -264,7 +264,7 @@ def test_decode_append_without_workspace_is_reported_before_the_cache_is_written
 @pytest.mark.parametrize("field,value,status", [
     ("seqlen_q", -1, pagedkv.PKV_EINVAL),
     ("mask", 4, pagedkv.PKV_EINVAL),
-    ("reserved2", 1, pagedkv.PKV_EINVAL),
+    ("kv_dtype", 7, pagedkv.PKV_EUNSUPPORTED),
     ("alibi_batch_stride", -1, pagedkv.PKV_EINVAL),
 ])
 def test_invalid_query_and_mask_fields_are_rejected(field, value, status):
@@ -288,8 +288,9 @@ def test_window_bounds_below_minus_one_are_rejected():
     assert pagedkv.workspace_size(d, 0) > 0
 
 
-def test_several_query_tokens_or_masks_need_the_mfma_path():
-    for kw in (dict(seqlen_q=4), dict(window_size=(64, -1)), dict(alibi_slopes=4096)):
+def test_several_query_tokens_masks_or_fp8_caches_need_the_mfma_path():
+    for kw in (dict(seqlen_q=4), dict(window_size=(64, -1)), dict(alibi_slopes=4096),
+               dict(kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3)):
         d = base_desc(path=pagedkv.PKV_PATH_VALU, **kw)
         assert pagedkv.schedule_for(d, 0) == 0
         assert pagedkv.path_for(base_desc(**kw)) == pagedkv.PKV_PATH_MFMA
