@@ -807,45 +807,41 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
             }
         }
     };
-    // Counted loops without a mid-body exit: a `break` between the two halves
+    // Counted loops without a mid-body exit: a `break` between the stages
     // would be structurized through the loop header and make the compiler's
     // wait counts assume the just-issued prefetch is the tile being consumed.
     const int ntiles = (end - t + 15) >> 4;
-    // Per tile: stage the landed tile in LDS, immediately issue the prefetch
-    // into the freed registers (pinned there by a scheduling barrier), then
-    // compute.  The prefetch is in flight for the whole QK / softmax / PV.
-    TileRegs<D, FP8> ra;
-    load_tile<D, WIDE, FP8>(ra, p, win, win_base, t, end, true, lane, kvh);
-    if constexpr (DEPTH == 1) {
-        for (int k = 0; k < ntiles; ++k) {
-            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
-            ensure_window(t + 16);
-            load_tile<D, WIDE, FP8>(ra, p, win, win_base, t + 16, end, k + 1 < ntiles, lane, kvh);
+    // DEPTH tiles of loads in flight, in a ring of registers.  Per tile: stage
+    // the landed tile in LDS, immediately issue the prefetch of the tile DEPTH
+    // ahead into the freed registers (pinned there by a scheduling barrier),
+    // then compute.  Prefetches past the range load a dummy line instead, so
+    // every path issues the same loads and the wait counts stay exact.
+    TileRegs<D, FP8> r[DEPTH];
+    load_tile<D, WIDE, FP8>(r[0], p, win, win_base, t, end, true, lane, kvh);
+#pragma unroll
+    for (int d = 1; d < DEPTH; ++d) {
+        ensure_window(t + 16 * d);
+        load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * d, end, d < ntiles, lane, kvh);
+    }
+    int k = 0;
+    for (; k + DEPTH <= ntiles; k += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            stage_tile<D, FP8, Math::kBF16>(r[d], lds, lane);
+            ensure_window(t + 16 * DEPTH);
+            load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * DEPTH, end, k + d + DEPTH < ntiles, lane, kvh);
             __builtin_amdgcn_sched_barrier(0);
             Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
         }
-    } else {
-        TileRegs<D, FP8> rb;
-        ensure_window(t + 16);
-        load_tile<D, WIDE, FP8>(rb, p, win, win_base, t + 16, end, ntiles > 1, lane, kvh);
-        for (int k = 0; k + 2 <= ntiles; k += 2) {
-            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
-            ensure_window(t + 32);
-            load_tile<D, WIDE, FP8>(ra, p, win, win_base, t + 32, end, k + 2 < ntiles, lane, kvh);
-            __builtin_amdgcn_sched_barrier(0);
+    }
+    // The last ntiles % DEPTH tiles: already loaded, nothing left to prefetch.
+#pragma unroll
+    for (int d = 0; d + 1 < DEPTH; ++d) {
+        if (k + d < ntiles) {
+            stage_tile<D, FP8, Math::kBF16>(r[d], lds, lane);
             Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
-            stage_tile<D, FP8, Math::kBF16>(rb, lds, lane);
-            ensure_window(t + 32);
-            load_tile<D, WIDE, FP8>(rb, p, win, win_base, t + 32, end, k + 3 < ntiles, lane, kvh);
-            __builtin_amdgcn_sched_barrier(0);
-            Math::tile(q, acc, lds, t, end, lane, scale_log2);
-            t += 16;
-        }
-        if (ntiles & 1) {
-            stage_tile<D, FP8, Math::kBF16>(ra, lds, lane);
-            Math::tile(q, acc, lds, t, end, lane, scale_log2);
         }
     }
 }
@@ -897,7 +893,7 @@ template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
 __global__ __launch_bounds__(64 * kWavesPerGroup) __attribute__((amdgpu_waves_per_eu(1)))
 void partition_split_kernel(PartitionParams p) {
     constexpr int kWaves = kWavesPerGroup;
-    static_assert(DEPTH == 1 || DEPTH == 2, "prefetch depth");
+    static_assert(DEPTH >= 1, "prefetch depth");
     __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[kWaves][2 * VTile<D>::kElems];
 
     const int wave = threadIdx.x >> 6;
@@ -1148,9 +1144,12 @@ constexpr int kSplitDepthFewItems = 2;
 // loading as one 16-bit tile.  Measured on MI355X (C2 / C3 / C4 / C5 with FP8
 // caches): 40.1 / 164 / 187 / 112 us with one tile, 32.6 / 129 / 134 / 111 us
 // with two; eight waves per CU instead of four gave 32.9 / 132 / 140 / 118.
+#ifndef PKV_FP8_DEPTH
+#define PKV_FP8_DEPTH 2
+#endif
 template <bool FP8>
 constexpr int kv_depth() {
-    return FP8 ? 2 : PKV_MFMA_DEPTH;
+    return FP8 ? PKV_FP8_DEPTH : PKV_MFMA_DEPTH;
 }
 
 template <typename Math, int D, bool WIDE, bool FP8>
