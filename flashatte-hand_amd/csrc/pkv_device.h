@@ -416,9 +416,13 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
 }
 
 
-// Worker owning tile x.
+// Worker owning tile x: floor(((x + 1) W - 1) / T), in 32 bits when it fits.
 __device__ __forceinline__ int32_t tile_worker_of(int64_t x, int64_t total, int32_t workers) {
-    return static_cast<int32_t>(((x + 1) * workers - 1) / total);
+    const uint64_t n = static_cast<uint64_t>(x + 1) * static_cast<uint64_t>(workers) - 1;
+    if (n < (1ull << 32) && total < (int64_t{1} << 32)) {
+        return static_cast<int32_t>(static_cast<uint32_t>(n) / static_cast<uint32_t>(total));
+    }
+    return static_cast<int32_t>(n / static_cast<uint64_t>(total));
 }
 
 // Row holding stream-unit index y (0 <= y < sum_b units_b): b, its clamped

@@ -30,6 +30,8 @@
 // re-tiled here for 64-lane MFMA with PV also on MFMA.
 #pragma once
 
+#include <type_traits>
+
 #include "pkv_device.h"
 #include "pkv_launch.h"
 
@@ -65,30 +67,53 @@ __device__ __forceinline__ f32x4 mfma_pv(const uint2& a, const uint2& b, f32x4 c
 }
 
 // Cache element width: 2 bytes (fp16 / bf16, the compute dtype) or 1 byte
-// (OCP FP8 e4m3, converted to the compute dtype when staged).
+// (OCP FP8 e4m3, converted to the compute dtype when staged).  Either way a
+// lane takes 8 elements of a token row (16 or 8 bytes), so the staged LDS
+// tile has one layout: each lane writes the 16-byte chunk of compute-dtype
+// values the 16-bit path writes, which is free of bank conflicts.  (Loading
+// 16 FP8 values per lane and writing the converted 32 bytes as two chunks
+// hit half the banks per write: 2.2 M conflict cycles per C2 launch.)
 template <int D, bool FP8>
 struct TileRegs {
     static constexpr int kBytes = FP8 ? 1 : 2; // bytes per cache element
-    static constexpr int L = D * kBytes / 16;  // lanes per token row (16 bytes each)
+    static constexpr int L = D / 8;            // lanes per token row
     static constexpr int R = 64 / L;           // tokens per load instruction
     static constexpr int NI = 16 / R;          // loads per tile and tensor
-    uint4 k[NI];
-    uint4 v[NI];
+    using Chunk = typename std::conditional<FP8, uint2, uint4>::type;
+    Chunk k[NI];
+    Chunk v[NI];
 };
 
+// One lane's chunk of a token row: 16 bytes of 16-bit values, or 8 FP8 bytes;
+// nontemporal (the cache is streamed once).
+template <bool FP8>
+__device__ __forceinline__ typename TileRegs<64, FP8>::Chunk load_chunk(const char* ptr) {
+    if constexpr (FP8) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(ptr));
+        return make_uint2(v.x, v.y);
+    } else {
+        return load_kv16(reinterpret_cast<const uint16_t*>(ptr));
+    }
+}
+
 // Issue the K and V loads of the 16-token tile starting at t0 in row layout:
-// the L = D/8 lanes of a row read one token's D contiguous 16-bit values of
-// this KV head (whole 128-byte lines), so one instruction covers R = 64/L
-// tokens and a tile takes D/32 instructions per tensor.  (Reading the MFMA
+// the L = D/8 lanes of a row read one token's D contiguous values of this KV
+// head (16 bytes per lane for 16-bit caches, 8 for FP8; whole 128-byte lines),
+// so one instruction covers R = 64/L tokens and a tile takes D/32
+// instructions per tensor.  (Reading the MFMA
 // operand layout straight from HBM — 16 tokens x 64 bytes per instruction —
 // streams measurably slower, so K is re-laid out through LDS instead.)
 // WIDE: P >= 16, so the tile lies inside one page whose id is wave-uniform and
 // is read from the page window with readlane; otherwise each lane fetches its
 // own token's page id from the window with ds_bpermute.  Neither waits on a
 // global load, so earlier tiles' loads stay in flight.  When `real` is false
-// (a prefetch past the end of the range) every lane loads the same 16 bytes at
-// the start of the caches instead: the loop then issues the same number of
-// loads on every path, which keeps the compiler's wait counts exact.
+// (a prefetch past the end of the range) every lane loads the same line at the
+// start of the caches instead: the loop then issues the same number of loads
+// on every path, which keeps the compiler's wait counts exact.  (Buffer loads
+// through a per-tile descriptor — one 32-bit offset per lane, rows past the
+// range read as zeros — cut the loop's VALU from 86 to 67 per tile but
+// measured 1-4 % slower.)
 template <int D, bool WIDE, bool FP8>
 __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionParams& p, int win, int win_base,
                                           int t0, int end, bool real, int lane, int kvh) {
@@ -99,10 +124,10 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
     constexpr int NI = Regs::NI;
     const int rl = lane / L;
     const int pmask = (1 << p.page_shift) - 1;
-    const uint32_t col = static_cast<uint32_t>(kvh * D * EB + 16 * (lane % L)); // bytes within a token row
+    const uint32_t col = static_cast<uint32_t>((kvh * D + 8 * (lane % L)) * EB); // bytes within a token row
     const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * EB;            // bytes per token
     if constexpr (WIDE) {
-        // Wave-uniform page base (SGPRs) + 32-bit lane offsets: saddr-form loads.
+        // Wave-uniform page base (SGPRs) + 32-bit lane offsets.
         const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
         const int phys = __builtin_amdgcn_readlane(win, idx);
         const int64_t base =
@@ -114,8 +139,8 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const uint32_t off = real ? static_cast<uint32_t>(min(R * i + rl, lim)) * ts2 + col : 0u;
-            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(kb + off));
-            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(vb + off));
+            r.k[i] = load_chunk<FP8>(kb + off);
+            r.v[i] = load_chunk<FP8>(vb + off);
         }
     } else {
 #pragma unroll
@@ -125,8 +150,8 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
             const int64_t off =
                 real ? static_cast<int64_t>(phys) * p.page_stride * EB + static_cast<int64_t>(t & pmask) * ts2 + col
                      : 0;
-            r.k[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.k) + off));
-            r.v[i] = load_kv16(reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(p.v) + off));
+            r.k[i] = load_chunk<FP8>(reinterpret_cast<const char*>(p.k) + off);
+            r.v[i] = load_chunk<FP8>(reinterpret_cast<const char*>(p.v) + off);
         }
     }
 }
@@ -156,17 +181,15 @@ __device__ __forceinline__ uint32_t fp8x2_to_16(uint32_t x) {
     }
 }
 
-// 16 FP8 values to 16 values of the compute dtype (two 16-byte chunks).
+// 8 FP8 values to 8 values of the compute dtype (one 16-byte chunk).
 template <bool BF16>
-__device__ __forceinline__ void fp8x16_to_16(const uint4& x, uint4& lo, uint4& hi) {
-    lo.x = fp8x2_to_16<BF16, false>(x.x);
-    lo.y = fp8x2_to_16<BF16, true>(x.x);
-    lo.z = fp8x2_to_16<BF16, false>(x.y);
-    lo.w = fp8x2_to_16<BF16, true>(x.y);
-    hi.x = fp8x2_to_16<BF16, false>(x.z);
-    hi.y = fp8x2_to_16<BF16, true>(x.z);
-    hi.z = fp8x2_to_16<BF16, false>(x.w);
-    hi.w = fp8x2_to_16<BF16, true>(x.w);
+__device__ __forceinline__ uint4 fp8x8_to_16(const uint2& x) {
+    uint4 r;
+    r.x = fp8x2_to_16<BF16, false>(x.x);
+    r.y = fp8x2_to_16<BF16, true>(x.x);
+    r.z = fp8x2_to_16<BF16, false>(x.y);
+    r.w = fp8x2_to_16<BF16, true>(x.y);
+    return r;
 }
 
 // Part 1a of a tile: stage the K and V rows in the wave's LDS tiles (FP8
@@ -180,23 +203,13 @@ __device__ __forceinline__ void stage_tile(const TileRegs<D, FP8>& r, uint16_t* 
     constexpr int NI = Regs::NI;
     uint16_t* kt = lds;
     uint16_t* vt = lds + VTile<D>::kElems;
-    if constexpr (FP8) {
-        const int wo = (lane / L) * VTile<D>::kRow + 16 * (lane % L);
+    const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            uint4 a;
-            uint4 b;
-            fp8x16_to_16<BF16>(r.k[i], a, b);
-            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = a;
-            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow + 8) = b;
-            fp8x16_to_16<BF16>(r.v[i], a, b);
-            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = a;
-            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow + 8) = b;
-        }
-    } else {
-        const int wo = (lane / L) * VTile<D>::kRow + 8 * (lane % L);
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
+    for (int i = 0; i < NI; ++i) {
+        if constexpr (FP8) {
+            *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = fp8x8_to_16<BF16>(r.k[i]);
+            *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = fp8x8_to_16<BF16>(r.v[i]);
+        } else {
             *reinterpret_cast<uint4*>(kt + wo + R * i * VTile<D>::kRow) = r.k[i];
             *reinterpret_cast<uint4*>(vt + wo + R * i * VTile<D>::kRow) = r.v[i];
         }
