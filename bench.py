@@ -191,9 +191,10 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     part_alg += kv_bytes - cfg.kv_bytes()                                   # window: visible keys only
     part_avg_ms = sum(part_ms) / K
     achieved = part_alg / (part_avg_ms * 1e-3) / 1e9
-    # The committed counter summary is for the one-query, unmasked decode.
-    plain = M == 1 and tuple(args.window) == (-1, -1) and not fp8
-    traffic = load_traffic(name, "mfma" if path == pagedkv.PKV_PATH_MFMA else "valu") if plain else None
+    # The committed counter summaries are for the one-query, unmasked decode (16-bit or FP8 caches).
+    plain = M == 1 and tuple(args.window) == (-1, -1)
+    kind = ("mfma" if path == pagedkv.PKV_PATH_MFMA else "valu") + ("_fp8" if fp8 else "")
+    traffic = load_traffic(name, kind) if plain else None
     res = {
         "config": cfg,
         "ms_per_step": ms_per_step,
