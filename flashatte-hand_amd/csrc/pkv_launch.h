@@ -28,10 +28,11 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_
     }
 }
 
-// Partition kernels (pkv_partition.hip): MFMA math (16 heads per wave,
-// zero-padded) or VALU math (heads_per_wave in {1, 2, 4}); head_dim in
-// {64, 128, 256}; the tile-balanced kernel when p.tile_workers > 0, else the
-// split-schedule kernel.
+// Partition kernels (pkv_partition_impl.h, one translation unit per head_dim):
+// MFMA math (heads_per_wave 16 or 32 query rows, zero-padded; several query
+// tokens, masks and FP8 caches) or VALU math (heads_per_wave in {1, 2, 4};
+// one query token, 16-bit caches); head_dim in {64, 128, 256}; the
+// tile-balanced kernel when p.tile_workers > 0, else the split-schedule kernels.
 hipError_t launch_partition(const PartitionParams& p, bool mfma, bool bf16, int head_dim, int heads_per_wave,
                             hipStream_t stream, const LaunchEvents& ev);
 

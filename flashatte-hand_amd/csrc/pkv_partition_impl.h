@@ -1,21 +1,26 @@
 // pkv_partition_impl.h — partition kernels for paged-KV GQA decode on gfx950
 // (templates; instantiated per head_dim by pkv_part_d{64,128,256}.hip).
 //
-// One wave64 works on one head slice (one kv head and up to Math::kHeads of its
-// query heads) over a token range, in tiles of 16 tokens.  Per tile:
+// One wave64 works on one slice of query rows (one kv head and up to
+// Math::kHeads of its query rows: heads, or (query token, head) pairs when
+// several query tokens share the cache) over a token range, in tiles of 16
+// tokens.  Per tile:
 //
 //   load   K and V rows in row layout (D/8 lanes per token, whole 128-byte
-//          lines, nontemporal 16-byte loads), page ids from a register window;
-//   stage  the rows into the wave's LDS tiles, then issue the next tile's
-//          loads into the freed registers (one tile in flight during compute);
-//   math   QK, online softmax (fp32, log2 domain, lazy rescale) and PV on the
-//          staged tile, by one of two policies:
-//     MfmaMath  16 heads per wave (zero-padded).  S^T[16 tok x 16 heads] =
-//               K Q^T with v_mfma_f32_16x16x32_{bf16,f16} (A = K from LDS,
-//               lane (n, j): token n, dims 8(4kk + j) .. +7; B = Q^T in VGPRs),
-//               then O^T[D x 16 heads] += V^T P^T with
+//          lines, nontemporal loads of 16 bytes, or 8 for FP8 caches), page
+//          ids from a register window;
+//   stage  the rows into the wave's LDS tiles (FP8 converted to the compute
+//          dtype), then issue the loads of the tile DEPTH ahead into the
+//          freed registers (a ring of DEPTH tiles in flight during compute);
+//   math   QK, online softmax (fp32, log2 domain, lazy rescale, optional
+//          masks / ALiBi) and PV on the staged tile, by one of two policies:
+//     MfmaMath  16 or 32 query rows per wave (zero-padded).  S^T[16 tok x 16
+//               rows] = K Q^T with v_mfma_f32_16x16x32_{bf16,f16} (A = K from
+//               LDS, lane (n, j): token n, dims 8(4kk + j) .. +7; B = Q^T in
+//               VGPRs), then O^T[D x 16 rows] += V^T P^T with
 //               v_mfma_f32_16x16x16{bf16_1k,f16}, V^T from the LDS tile through
-//               ds_read_b64_tr_b16 and P^T packed to 16 bits in place;
+//               ds_read_b64_tr_b16 and P^T packed to 16 bits in place; a second
+//               block of 16 rows reuses the same K and V^T operands;
 //     ValuMath  1, 2 or 4 heads per wave.  Lane (t, c) takes token t and a
 //               quarter of the dims: v_dot2 products, a cross-row sum, DPP row
 //               max/sum; PV with fp32 FMAs, each lane owning D/64 dims of
