@@ -339,6 +339,17 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.rows = static_cast<int32_t>(r.B * r.M * r.H);
         c.q_len = p.q_len;
         c.win_left = p.win_left;
+        // Streams split over a few workers (about workers / streams + 1 parts
+        // each, within the stream combine's first round trip) are merged four
+        // rows per wave when that still makes at least 8 waves per CU: fewer,
+        // fuller waves.  Otherwise a row per wave.  Measured: C4 8.2 -> 6.4 us
+        // and C4 with four query tokens 22 -> 13.9 us by stream; C2 (256 waves)
+        // 4.1 -> 6.6, C2 with four query tokens (1,024) 4.8 -> 7.0 and C5's
+        // five-part streams 6.6 -> 8.5 us would lose.
+        const int64_t streams = r.B * streams_per_row(r);
+        const int64_t parts_est = plan.splits / std::max<int64_t>(streams, 1) + 1;
+        const int64_t stream_waves = streams * ((p.part_heads + pkv::kStreamRows - 1) / pkv::kStreamRows);
+        c.by_stream = tiles && stream_waves >= 8 * kComputeUnits && parts_est <= 1024 / r.D ? 1 : 0;
         c.num_heads = static_cast<int32_t>(r.H);
         c.splits = splits;
         c.split_tokens = plan.split_tokens;

@@ -278,11 +278,188 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     }
 }
 
+// Tile-balanced schedule, few parts per stream: one wave per block of
+// kStreamRows query rows of a stream.  The stream's workers are located once
+// for the block, and the LSEs and first partial rows of all its rows are
+// loaded together (one round trip for all of them), so the grid has one wave
+// per stream block instead of one per output row: 4-8x fewer waves to
+// dispatch, the same loads.  Long streams (many parts) use
+// combine_tiles_kernel, whose waves take one row each.  (kStreamRows rows per
+// wave, pkv_device.h.)
+
+template <bool BF16, int D>
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(CombineParams p) {
+    constexpr int E = D / 64;
+    constexpr int RB = kStreamRows;
+    constexpr int KB = 16 / E; // partial rows per query row and round trip (divides 64)
+    const int lane = threadIdx.x & 63;
+    const int wid = static_cast<int>(blockIdx.x) * kCombineWaves + static_cast<int>(threadIdx.x >> 6);
+    const int spr = (p.num_heads / p.group) * p.head_groups;
+    const int blocks = (p.part_heads + RB - 1) / RB;
+    const int s = wid / blocks;
+    if (s >= p.batch * spr) {
+        return;
+    }
+    const int b = s / spr;
+    const int u = s - b * spr;
+    const int kvh = u / p.head_groups;
+    const int hg = u - kvh * p.head_groups;
+    const int r_first = (wid - s * blocks) * RB; // first row of the block within the stream
+    const int rows_here = min(RB, min(p.heads_per_wave, p.q_len * p.group - hg * p.heads_per_wave) - r_first);
+    if (rows_here <= 0) {
+        return;
+    }
+    // Output row of stream row r: query row qr = i * group + g of (b, kvh).
+    auto out_row = [&](int r) -> int64_t {
+        const int qr = hg * p.heads_per_wave + r_first + r;
+        const int i = qr / p.group;
+        const int g = qr - i * p.group;
+        return (static_cast<int64_t>(b) * p.q_len + i) * p.num_heads + kvh * p.group + g;
+    };
+
+    const int nb = row_tiles(p.seqlens, b, p.row_cap, p.q_len, p.win_left);
+    if (nb == 0) {
+        for (int r = 0; r < rows_here; ++r) {
+            uint16_t* dst = p.out + out_row(r) * D + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                dst[e] = 0;
+            }
+        }
+        return;
+    }
+    int64_t before = 0;
+    int64_t all = 0;
+    for (int32_t bb = lane; bb < p.batch; bb += 64) {
+        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left));
+        all += t;
+        before += bb < b ? t : 0;
+    }
+    before = uniform(wave_sum_i64(before));
+    const int64_t total = uniform(static_cast<int64_t>(spr) * wave_sum_i64(all));
+    const int64_t first =
+        static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
+    const TilePlan plan = make_tile_plan(total, p.tile_workers);
+    const int32_t wa = tile_worker_of(first, plan.total, plan.workers);
+    const int32_t wb = tile_worker_of(first + nb - 1, plan.total, plan.workers);
+    if (wa == wb) {
+        return; // one worker: the partition wrote these rows
+    }
+    const int parts = wb - wa + 1;
+    const int64_t slot0 = static_cast<int64_t>(wa) + static_cast<int64_t>(b) * spr + u;
+    // Row r's part k: LSE at (slot0 + k) * part_heads + r_first + r, O row likewise.
+    const float* __restrict__ lse = p.part_lse + slot0 * p.part_heads + r_first;
+    const float* __restrict__ po = p.part_o + (slot0 * p.part_heads + r_first) * D + lane * E;
+    const int64_t ls = p.part_heads;
+    const int64_t os = static_cast<int64_t>(p.part_heads) * D;
+
+    // One round trip: every row's first 64 LSEs (lane k: part k) and first KB partial rows.
+    float l0[RB];
+    float x[RB][KB][E];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const bool live = r < rows_here;
+        l0[r] = (live && lane < parts) ? lse[lane * ls + r] : kNegInf;
+#pragma unroll
+        for (int v = 0; v < KB; ++v) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                x[r][v][e] = 0.f;
+            }
+            if (live && v < parts) {
+                load_partial<E>(po + v * os + r * D, x[r][v]);
+            }
+        }
+    }
+    float wl[RB];
+    float den[RB];
+    float acc[RB][E];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        float mx = l0[r];
+        for (int k = lane + 64; k < parts; k += 64) {
+            mx = fmaxf(mx, r < rows_here ? lse[k * ls + r] : kNegInf);
+        }
+        mx = group_max<64>(mx);
+        // A part whose rows saw no visible key (masks) has lse = -inf and
+        // weighs 0, also when every part is empty (mx = -inf).
+        wl[r] = (lane < parts && l0[r] != kNegInf) ? fast_exp2(l0[r] - mx) : 0.f;
+        den[r] = wl[r];
+        l0[r] = mx; // keep the row's max for the weights of parts past 64
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            acc[r][e] = 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < KB; ++v) {
+            const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[r]), v));
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                acc[r][e] = fmaf(wv, x[r][v][e], acc[r][e]); // x = 0 past the last part
+            }
+        }
+    }
+    // Streams with more than KB parts: the rest, KB partial rows of every row per round trip.
+#pragma unroll 1
+    for (int k = KB; k < parts; k += KB) {
+        if ((k & 63) == 0) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                const int kl = k + lane;
+                const float lk = (r < rows_here && kl < parts) ? lse[kl * ls + r] : kNegInf;
+                wl[r] = lk != kNegInf ? fast_exp2(lk - l0[r]) : 0.f;
+                den[r] += wl[r];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+#pragma unroll
+            for (int v = 0; v < KB; ++v) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    x[r][v][e] = 0.f;
+                }
+                if (r < rows_here && k + v < parts) {
+                    load_partial<E>(po + (k + v) * os + r * D, x[r][v]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+#pragma unroll
+            for (int v = 0; v < KB; ++v) {
+                const float wv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl[r]), (k + v) & 63));
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    acc[r][e] = fmaf(wv, x[r][v][e], acc[r][e]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const float d = group_sum<64>(den[r]);
+        if (r < rows_here) {
+            const float inv = d > 0.f ? 1.f / d : 0.f;
+            uint16_t* dst = p.out + out_row(r) * D + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                dst[e] = from_f32<BF16>(acc[r][e] * inv);
+            }
+        }
+    }
+}
+
 template <bool BF16, int D>
 static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, const LaunchEvents& ev) {
     constexpr int kWaves = kCombineWaves;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
-    if (p.tile_workers > 0) {
+    if (p.tile_workers > 0 && p.by_stream) {
+        const int spr = (p.num_heads / p.group) * p.head_groups;
+        const int waves = p.batch * spr * ((p.part_heads + kStreamRows - 1) / kStreamRows);
+        launch_kernel(combine_streams_kernel<BF16, D>, dim3((waves + kWaves - 1) / kWaves), dim3(64 * kWaves), 0,
+                      stream, ev, p);
+    } else if (p.tile_workers > 0) {
         launch_kernel(combine_tiles_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else {
         launch_kernel(combine_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);

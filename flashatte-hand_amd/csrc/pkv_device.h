@@ -77,7 +77,11 @@ struct CombineParams {
     int32_t heads_per_wave; // query rows per stream (16 MFMA, 1/2/4 VALU)
     int32_t q_len;        // as in PartitionParams; rows = B * q_len * H
     int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
+    int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
 };
+
+// Query rows per wave of the tile schedule's stream combine.
+constexpr int kStreamRows = 4;
 
 // Paged KV-cache append (pkv_append.hip): one 16-byte chunk of K and of V per
 // thread.  A token row is Hk * D 16-bit elements, contiguous in the new-token
