@@ -502,34 +502,61 @@ __device__ __forceinline__ int64_t wave_inclusive_scan(int64_t x, int32_t lane) 
     return x;
 }
 
-// Units per row of the call, as a wave-wide prefix.  Rows 0..63 are read once
-// and kept in registers; larger batches add a sum over the remaining rows, and
-// locating a unit in them takes a chunked pass (locate_row).  Batches of up to
-// 64 rows whose unit counts fit 32 bits use a 32-bit DPP scan.
+// Units per row of the call, as a wave-wide prefix.  Up to kScanChunks * 64
+// rows are read once (one load per lane and chunk, all issued together) and
+// kept in registers, each chunk scanned in 32 bits with DPP and the chunks
+// chained by uniform carries, so locating a unit is a ballot per chunk with no
+// further memory access.  Larger batches add a sum over the remaining rows,
+// and locating a unit in them takes a chunked pass that reads cache_seqlens
+// again (locate_row).
+constexpr int kScanChunks = 4;
+
 struct RowScan {
-    int64_t rows_total; // sum over rows of stream_units(n_b)
-    bool fast;          // incl holds the whole prefix (batch <= 64, 32-bit)
-    uint32_t incl;      // lane b: sum of stream_units(n_b') for b' <= b (fast path)
-    int32_t sl0;        // lane b: clamped seqlen of row b (b < 64)
-    int32_t n0;         // lane b: tiles of row b
+    int64_t rows_total;           // sum over rows of stream_units(n_b)
+    bool fast;                    // the chunks hold every row (batch <= 256, row_cap <= 2^24)
+    uint32_t incl[kScanChunks];   // lane: units of rows 64c .. 64c + lane (inclusive), within chunk c
+    int64_t carry[kScanChunks];   // units of the rows before chunk c (uniform)
+    int32_t sl[kScanChunks];      // lane: clamped seqlen of row 64c + lane
+    int32_t n[kScanChunks];       // lane: tiles of that row
 };
 
 __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens, int32_t batch, int32_t row_cap,
                                              int32_t q_len, int32_t win_left, int32_t lane) {
     RowScan rs;
-    rs.sl0 = lane < batch ? clamped_seqlen(seqlens, lane, row_cap) : 0;
-    rs.n0 = tile_span(rs.sl0, q_len, win_left).n;
-    // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so 64 rows of
-    // them fit 32 bits when row_cap <= 2^24.
-    rs.fast = batch <= 64 && row_cap <= (1 << 24);
+    // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so a chunk
+    // of 64 rows of them fits 32 bits when row_cap <= 2^24.
+    rs.fast = batch <= 64 * kScanChunks && row_cap <= (1 << 24);
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        const int32_t b = 64 * c + lane;
+        rs.sl[c] = (c == 0 || 64 * c < batch) && b < batch ? clamped_seqlen(seqlens, b, row_cap) : 0;
+        rs.n[c] = tile_span(rs.sl[c], q_len, win_left).n;
+    }
     if (rs.fast) {
-        rs.incl = wave_inclusive_scan_u32(static_cast<uint32_t>(stream_units(rs.n0)));
-        rs.rows_total = __builtin_amdgcn_readlane(rs.incl, 63);
+        int64_t carry = 0;
+#pragma unroll
+        for (int c = 0; c < kScanChunks; ++c) {
+            rs.carry[c] = carry;
+            rs.incl[c] = 0;
+            if (c == 0 || 64 * c < batch) {
+                rs.incl[c] = wave_inclusive_scan_u32(static_cast<uint32_t>(stream_units(rs.n[c])));
+                carry += __builtin_amdgcn_readlane(rs.incl[c], 63);
+            }
+        }
+        rs.rows_total = carry;
         return rs;
     }
-    rs.incl = 0;
-    int64_t sum = stream_units(rs.n0);
-    for (int32_t b = lane + 64; b < batch; b += 64) {
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        rs.incl[c] = 0;
+        rs.carry[c] = 0;
+    }
+    int64_t sum = 0;
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        sum += stream_units(rs.n[c]);
+    }
+    for (int32_t b = lane + 64 * kScanChunks; b < batch; b += 64) {
         sum += stream_units(row_tiles(seqlens, b, row_cap, q_len, win_left));
     }
     rs.rows_total = wave_sum_i64(sum);
@@ -541,14 +568,22 @@ __device__ __forceinline__ RowTiles locate_unit_row(const RowScan& rs, const int
                                                     int32_t batch, int32_t row_cap, int32_t q_len, int32_t win_left,
                                                     int64_t y, int32_t lane) {
     if (rs.fast) {
-        const uint64_t hit = __ballot(lane < batch && rs.incl > static_cast<uint32_t>(y));
-        const int32_t l = __builtin_ctzll(hit); // hit != 0 for y < rows_total
-        RowTiles r;
-        r.b = l;
-        r.seqlen = __shfl(rs.sl0, l, 64);
-        r.n = __shfl(rs.n0, l, 64);
-        r.before = static_cast<int64_t>(__builtin_amdgcn_readlane(rs.incl, l)) - stream_units(r.n);
-        return r;
+#pragma unroll
+        for (int c = 0; c < kScanChunks; ++c) {
+            const int64_t yc = y - rs.carry[c];
+            const uint64_t hit = __ballot(64 * c + lane < batch && yc >= 0 && yc < (int64_t{1} << 32) &&
+                                          rs.incl[c] > static_cast<uint32_t>(yc));
+            if (hit != 0) {
+                const int32_t l = __builtin_ctzll(hit);
+                RowTiles r;
+                r.b = 64 * c + l;
+                r.seqlen = __shfl(rs.sl[c], l, 64);
+                r.n = __shfl(rs.n[c], l, 64);
+                r.before = rs.carry[c] + static_cast<int64_t>(__builtin_amdgcn_readlane(rs.incl[c], l)) -
+                           stream_units(r.n);
+                return r;
+            }
+        }
     }
     return locate_row(seqlens, batch, row_cap, q_len, win_left, y, lane);
 }

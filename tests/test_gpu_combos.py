@@ -101,3 +101,18 @@ def test_clamped_and_negative_lengths_under_masks(rng, fp8):
         want = po.attn_f64(q, k, v, bt, sl, 0.1, dtype, causal=True, window=(20, 0))
         assert np.max(np.abs(po.bits_to_f32(from_dev(out), dtype) - want)) < TOL[dtype]
     assert np.all(po.bits_to_f32(from_dev(out), dtype)[1] == 0)
+
+
+@pytest.mark.parametrize("M,causal", [(1, False), (2, True)])
+def test_batch_past_the_register_scan(rng, M, causal):
+    """300 rows: more than the row scan keeps in registers (256), so locating a worker's
+    first row takes the chunked pass over cache_seqlens."""
+    announce("combo-batch300", M, causal)
+    B, H, Hk, D, P, dtype = 300, 8, 2, 64, 16, 1
+    lens = rng.integers(0, 200, B)
+    _, k, v, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=lens, dtype=dtype)
+    q = rand_bits(rng, (B, M, H, D), dtype)
+    for splits in (0, 1):
+        out = run(q, k, v, bt, sl, 0.125, dtype, splits, causal=causal)
+        want = po.attn_f64(q, k, v, bt, sl, 0.125, dtype, causal=causal)
+        assert np.max(np.abs(po.bits_to_f32(from_dev(out), dtype) - want)) < TOL[dtype], splits
