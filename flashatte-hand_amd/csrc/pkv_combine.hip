@@ -143,6 +143,32 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(CombinePara
     }
 }
 
+// Row b's tiles, and the stream units of the rows before b and of all rows
+// (tile-balanced schedule), from one pass over cache_seqlens: one round trip.
+struct RowUnits {
+    int32_t nb;
+    int64_t before;
+    int64_t all;
+};
+
+__device__ __forceinline__ RowUnits row_units(const CombineParams& p, int32_t b, int lane) {
+    int64_t before = 0;
+    int64_t all = 0;
+    int32_t nb = 0;
+    for (int32_t bb = lane; bb < p.batch; bb += 64) {
+        const int32_t n = row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left);
+        const int32_t t = stream_units(n);
+        all += t;
+        before += bb < b ? t : 0;
+        nb = bb == b ? n : nb;
+    }
+    RowUnits ru;
+    ru.nb = __builtin_amdgcn_readlane(nb, b & 63); // lane b % 64 saw row b
+    ru.before = uniform(wave_sum_i64(before));
+    ru.all = uniform(wave_sum_i64(all));
+    return ru;
+}
+
 // Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; the
 // workers w_a .. w_b owning its tiles are found from cache_seqlens with the
 // partition's unit arithmetic.  One worker means the partition already wrote
@@ -172,7 +198,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     const int u = kvh * p.head_groups + hg;
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
 
-    const int nb = row_tiles(p.seqlens, b, p.row_cap, p.q_len, p.win_left);
+    const RowUnits ru = row_units(p, b, lane);
+    const int nb = ru.nb;
     if (nb == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
@@ -180,15 +207,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
         }
         return;
     }
-    int64_t before = 0;
-    int64_t all = 0;
-    for (int32_t bb = lane; bb < p.batch; bb += 64) {
-        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left));
-        all += t;
-        before += bb < b ? t : 0;
-    }
-    before = uniform(wave_sum_i64(before));
-    const int64_t total = uniform(static_cast<int64_t>(spr) * wave_sum_i64(all));
+    const int64_t before = ru.before;
+    const int64_t total = static_cast<int64_t>(spr) * ru.all;
     // Unit of the stream's first tile.
     const int64_t first =
         static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
@@ -317,7 +337,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
         return (static_cast<int64_t>(b) * p.q_len + i) * p.num_heads + kvh * p.group + g;
     };
 
-    const int nb = row_tiles(p.seqlens, b, p.row_cap, p.q_len, p.win_left);
+    const RowUnits ru = row_units(p, b, lane);
+    const int nb = ru.nb;
     if (nb == 0) {
         for (int r = 0; r < rows_here; ++r) {
             uint16_t* dst = p.out + out_row(r) * D + lane * E;
@@ -328,15 +349,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
         }
         return;
     }
-    int64_t before = 0;
-    int64_t all = 0;
-    for (int32_t bb = lane; bb < p.batch; bb += 64) {
-        const int32_t t = stream_units(row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left));
-        all += t;
-        before += bb < b ? t : 0;
-    }
-    before = uniform(wave_sum_i64(before));
-    const int64_t total = uniform(static_cast<int64_t>(spr) * wave_sum_i64(all));
+    const int64_t before = ru.before;
+    const int64_t total = static_cast<int64_t>(spr) * ru.all;
     const int64_t first =
         static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
     const TilePlan plan = make_tile_plan(total, p.tile_workers);
