@@ -1,0 +1,744 @@
+// pkv_harness: the thin C++ host harness over HIP for the paged-KV decode
+// entry points, with no Python anywhere.  It has the shape of the reference's
+// evaluator (scripts/evaluate_flashattn_submission.py): build a case
+// (make_case, 105-151), run the candidate once and check it (evaluate_case,
+// 199-275), then time repeated calls between two events (time_cuda,
+// 152-165).  flash-attn is not available, so the check is this harness's
+// own: fp64 attention over sampled output rows, bit-exact invariants of the
+// paged layout, and agreement between the two entry points.
+//
+//   pkv_harness --config c1..c5            the five benchmark workloads
+//   pkv_harness --case B,S,M,H,Hk,D,P      an evaluator case (--profile legacy|contest)
+//   options: --entry pkv_decode|run_kernel  --dtype bf16|f16  --splits N  --causal
+//            --warmup W  --repeat R  --sets N  --seed S  --check
+//
+// Prints one JSON line; exit status 0 = ran (and checks passed), 1 = a check
+// failed, 2 = bad arguments or a HIP / library error.
+
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/pkv_decode.h"
+
+namespace {
+
+[[noreturn]] void die(const std::string& msg) {
+    std::fprintf(stderr, "pkv_harness: %s\n", msg.c_str());
+    std::exit(2);
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        die(std::string(what) + ": " + hipGetErrorString(e));
+    }
+}
+
+// ------------------------------------------------------------------ random numbers
+// splitmix64 (Steele, Lea and Flood 2014) as the seeded generator; normals by
+// Box-Muller.  The device fill hashes the element index with the same mixer,
+// so every element is a pure function of (seed, index).
+
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+
+struct Rng {
+    uint64_t s;
+    uint64_t next() { return mix64(s += kGolden); }
+    double uniform() { return static_cast<double>(next() >> 11) * 0x1.0p-53; } // [0, 1)
+    int64_t range(int64_t lo, int64_t hi) {                                      // [lo, hi]
+        const uint64_t n = static_cast<uint64_t>(hi - lo + 1);
+        return lo + static_cast<int64_t>(static_cast<unsigned __int128>(next()) * n >> 64);
+    }
+    double normal() {
+        const double u1 = 1.0 - uniform(); // (0, 1]
+        const double u2 = uniform();
+        return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+    }
+    template <typename T>
+    void shuffle(std::vector<T>& v) {
+        for (size_t i = v.size(); i > 1; --i) {
+            std::swap(v[i - 1], v[static_cast<size_t>(range(0, static_cast<int64_t>(i) - 1))]);
+        }
+    }
+};
+
+__device__ inline float hash_normal(uint64_t seed, uint64_t i) {
+    const uint64_t a = mix64(seed + (2 * i + 1) * kGolden);
+    const uint64_t b = mix64(seed + (2 * i + 2) * kGolden);
+    const float u1 = 1.0f - static_cast<float>(a >> 40) * 0x1.0p-24f; // (0, 1]
+    const float u2 = static_cast<float>(b >> 40) * 0x1.0p-24f;
+    return sqrtf(-2.0f * logf(u1)) * cosf(6.2831853f * u2);
+}
+
+// n elements of N(0, sigma) as 16-bit values; with peak_prob > 0 each row of
+// `row` elements is scaled by peak_factor with that probability.
+__global__ void fill_normal_kernel(uint16_t* dst, int64_t n, int row, uint64_t seed, float sigma, float peak_prob,
+                                   float peak_factor, int bf16) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    float x = sigma * hash_normal(seed, static_cast<uint64_t>(i));
+    if (peak_prob > 0.f) {
+        const uint64_t r = static_cast<uint64_t>(i / row);
+        const float u = static_cast<float>(mix64(~seed + r * kGolden) >> 40) * 0x1.0p-24f;
+        x = u < peak_prob ? x * peak_factor : x;
+    }
+    if (bf16) {
+        const __hip_bfloat16 h = __float2bfloat16(x);
+        dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+    } else {
+        const __half h = __float2half(x);
+        dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+    }
+}
+
+// dst page perm[p] = src page p (pages of page_elems 16-bit elements).
+__global__ void permute_pages_kernel(const uint16_t* src, uint16_t* dst, const int32_t* perm, int64_t pages,
+                                     int64_t page_elems) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= pages * page_elems) {
+        return;
+    }
+    const int64_t p = i / page_elems;
+    dst[static_cast<int64_t>(perm[p]) * page_elems + (i - p * page_elems)] = src[i];
+}
+
+int64_t blocks_for(int64_t n, int threads) { return (n + threads - 1) / threads; }
+
+// ------------------------------------------------------------------ 16-bit values on the host
+
+double bits_to_double(uint16_t v, bool bf16) {
+    if (bf16) {
+        const uint32_t w = static_cast<uint32_t>(v) << 16;
+        float f;
+        std::memcpy(&f, &w, 4);
+        return f;
+    }
+    const int sign = v >> 15;
+    const int exp = (v >> 10) & 31;
+    const int man = v & 1023;
+    double mag;
+    if (exp == 0) {
+        mag = std::ldexp(static_cast<double>(man), -24);
+    } else if (exp == 31) {
+        mag = man ? NAN : INFINITY;
+    } else {
+        mag = std::ldexp(static_cast<double>(man + 1024), exp - 25);
+    }
+    return sign ? -mag : mag;
+}
+
+// ------------------------------------------------------------------ cases
+
+struct Case {
+    std::string name;
+    int64_t B = 1, M = 1, H = 8, Hk = 2, D = 128, P = 16;
+    bool bf16 = true;
+    bool causal = false;
+    std::vector<int32_t> seqlens;
+    std::vector<int32_t> bt; // [B, stride]
+    int64_t stride = 0;
+    int64_t num_pages = 0;
+    float q_sigma = 1.f, kv_sigma = 1.f, k_peak_prob = 0.f;
+    int num_splits = 0;
+    int64_t max_seqlen() const { return *std::max_element(seqlens.begin(), seqlens.end()); }
+    int64_t kv_bytes() const {
+        int64_t t = 0;
+        for (int32_t s : seqlens) {
+            t += std::max(s, 0);
+        }
+        return t * Hk * D * 2 * 2;
+    }
+};
+
+int64_t pages_of(int64_t len, int64_t P) { return (std::max<int64_t>(len, 0) + P - 1) / P; }
+
+// Rows draw their pages without replacement from one shuffled pool of
+// `pool` pages; entries past a row's last page hold page 0.
+void scatter_table(Case& c, Rng& rng, int64_t pool) {
+    int64_t need = 0;
+    c.stride = 1;
+    for (int32_t s : c.seqlens) {
+        need += pages_of(s, c.P);
+        c.stride = std::max(c.stride, pages_of(s, c.P));
+    }
+    if (pool < need) {
+        die("page pool smaller than the rows' pages");
+    }
+    std::vector<int32_t> perm(static_cast<size_t>(pool));
+    for (int64_t i = 0; i < pool; ++i) {
+        perm[static_cast<size_t>(i)] = static_cast<int32_t>(i);
+    }
+    rng.shuffle(perm);
+    c.num_pages = pool;
+    c.bt.assign(static_cast<size_t>(c.B * c.stride), 0);
+    int64_t next = 0;
+    for (int64_t b = 0; b < c.B; ++b) {
+        for (int64_t j = 0; j < pages_of(c.seqlens[static_cast<size_t>(b)], c.P); ++j) {
+            c.bt[static_cast<size_t>(b * c.stride + j)] = perm[static_cast<size_t>(next++)];
+        }
+    }
+}
+
+// The benchmark workloads: geometry, dtypes and value laws as specified, with
+// this harness's own generator (so row lengths differ from other drivers'
+// draws of the same laws).  Open choices: C2 pool = ceil(1.25 x pages);
+// C4 log-normal sigma = 1; C5 rows 0 and 1 forced to 1 and 8191.
+Case make_config(const std::string& name, uint64_t seed) {
+    Case c;
+    c.name = name;
+    Rng rng{seed};
+    if (name == "c1") {
+        c.B = 1, c.H = 8, c.Hk = 2, c.D = 128, c.P = 16, c.bf16 = false, c.num_splits = 1;
+        c.seqlens = {256};
+        std::vector<int32_t> perm(32);
+        for (int i = 0; i < 32; ++i) {
+            perm[static_cast<size_t>(i)] = i;
+        }
+        rng.shuffle(perm);
+        c.stride = 16, c.num_pages = 32;
+        c.bt.assign(perm.begin(), perm.begin() + 16);
+        return c;
+    }
+    if (name == "c2") {
+        c.B = 32, c.H = 32, c.Hk = 8, c.D = 128, c.P = 64, c.bf16 = true;
+        int64_t pages = 0;
+        for (int64_t b = 0; b < c.B; ++b) {
+            c.seqlens.push_back(static_cast<int32_t>(rng.range(512, 4096)));
+            pages += pages_of(c.seqlens.back(), c.P);
+        }
+        scatter_table(c, rng, (pages * 5 + 3) / 4);
+    } else if (name == "c3") {
+        c.B = 4, c.H = 32, c.Hk = 8, c.D = 128, c.P = 64, c.bf16 = false, c.k_peak_prob = 0.01f;
+        c.seqlens = {32768, 65536, 100000, 131072};
+        int64_t pages = 0;
+        for (int32_t s : c.seqlens) {
+            pages += pages_of(s, c.P);
+        }
+        scatter_table(c, rng, pages);
+    } else if (name == "c4") {
+        c.B = 128, c.H = 64, c.Hk = 8, c.D = 128, c.P = 32, c.bf16 = true;
+        int64_t pages = 0;
+        for (int64_t b = 0; b < c.B; ++b) {
+            const double x = std::exp(std::log(2048.0) + rng.normal());
+            c.seqlens.push_back(static_cast<int32_t>(std::clamp(std::llround(x), 1LL, 16384LL)));
+            pages += pages_of(c.seqlens.back(), c.P);
+        }
+        scatter_table(c, rng, pages);
+    } else if (name == "c5") {
+        c.B = 256, c.H = 16, c.Hk = 1, c.D = 256, c.P = 16, c.bf16 = false, c.q_sigma = 0.5f, c.kv_sigma = 0.5f;
+        int64_t pages = 0;
+        for (int64_t b = 0; b < c.B; ++b) {
+            c.seqlens.push_back(b == 0 ? 1 : b == 1 ? 8191 : static_cast<int32_t>(rng.range(1, 8192)));
+            pages += pages_of(c.seqlens.back(), c.P);
+        }
+        scatter_table(c, rng, pages);
+    } else {
+        die("unknown config " + name + " (c1 .. c5)");
+    }
+    return c;
+}
+
+// The evaluator's make_case (evaluate_flashattn_submission.py:105-151):
+// "legacy" = every row at S tokens in a pool of max(1024, 3 B ceil(S / P))
+// pages rounded up to a multiple of B; "contest" = a pool of exactly
+// B ceil(S / P) pages with row 0 at S, row 1 at 1 and row b at
+// 1 + ((9973 b + S / 3) mod max(1, S - 1)).  block_table is a random
+// permutation of the pool, B rows of num_pages / B entries.
+Case make_eval_case(int64_t B, int64_t S, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t P, bool contest,
+                    uint64_t seed) {
+    Case c;
+    c.name = contest ? "contest" : "legacy";
+    c.B = B, c.M = M, c.H = H, c.Hk = Hk, c.D = D, c.P = P;
+    const int64_t bpb = (S + P - 1) / P;
+    int64_t pool = bpb * B;
+    if (!contest) {
+        pool = std::max<int64_t>(1024, 3 * pool);
+        pool += (B - pool % B) % B;
+    }
+    for (int64_t b = 0; b < B; ++b) {
+        int64_t s = S;
+        if (contest && b == 1) {
+            s = 1;
+        } else if (contest && b > 1) {
+            s = 1 + (b * 9973 + S / 3) % std::max<int64_t>(1, S - 1);
+        }
+        c.seqlens.push_back(static_cast<int32_t>(s));
+    }
+    Rng rng{seed};
+    std::vector<int32_t> perm(static_cast<size_t>(pool));
+    for (int64_t i = 0; i < pool; ++i) {
+        perm[static_cast<size_t>(i)] = static_cast<int32_t>(i);
+    }
+    rng.shuffle(perm);
+    c.bt = perm;
+    c.num_pages = pool;
+    c.stride = pool / B;
+    return c;
+}
+
+// run_kernel's fixed conventions: bf16, heuristic splits and block_table
+// rows of num_blocks / batch_size entries (best_flashattn_kvcache_decode.cu:1213-1215).
+bool legacy_entry_fits(const Case& c) { return c.bf16 && c.num_splits == 0 && c.stride == c.num_pages / c.B; }
+
+// ------------------------------------------------------------------ device state
+
+template <typename T>
+T* dev_alloc(size_t n) {
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)), "hipMalloc");
+    return static_cast<T*>(p);
+}
+
+template <typename T>
+void to_dev(T* dst, const std::vector<T>& src) {
+    hip_check(hipMemcpy(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+}
+
+template <typename T>
+std::vector<T> from_dev(const T* src, size_t n) {
+    std::vector<T> v(n);
+    hip_check(hipMemcpy(v.data(), src, n * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy D2H");
+    return v;
+}
+
+void fill(uint16_t* dst, int64_t n, int row, uint64_t seed, float sigma, float peak_prob, bool bf16) {
+    const int threads = 256;
+    fill_normal_kernel<<<dim3(static_cast<unsigned>(blocks_for(n, threads))), dim3(threads)>>>(
+        dst, n, row, seed, sigma, peak_prob, 8.0f, bf16 ? 1 : 0);
+    hip_check(hipGetLastError(), "fill kernel");
+}
+
+struct KvSet {
+    uint16_t* k = nullptr;
+    uint16_t* v = nullptr;
+    uint16_t* q = nullptr;
+    uint16_t* out = nullptr;
+};
+
+struct Runner {
+    const Case& c;
+    std::string entry;
+    int32_t* d_bt = nullptr;
+    int32_t* d_sl = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    pkv_decode_desc desc{};
+    float scale = 0.f;
+
+    Runner(const Case& cs, std::string e) : c(cs), entry(std::move(e)) {
+        d_bt = dev_alloc<int32_t>(c.bt.size());
+        d_sl = dev_alloc<int32_t>(c.seqlens.size());
+        to_dev(d_bt, c.bt);
+        to_dev(d_sl, c.seqlens);
+        desc.batch = c.B;
+        desc.num_heads = c.H;
+        desc.num_heads_k = c.Hk;
+        desc.head_dim = c.D;
+        desc.page_size = c.P;
+        desc.num_pages = c.num_pages;
+        desc.block_table_stride = c.stride;
+        desc.max_seqlen = c.max_seqlen();
+        desc.dtype = c.bf16 ? PKV_DTYPE_BF16 : PKV_DTYPE_F16;
+        desc.path = PKV_PATH_AUTO;
+        desc.seqlen_q = c.M;
+        desc.mask = c.causal ? PKV_MASK_CAUSAL : 0;
+        scale = 1.0f / std::sqrt(static_cast<float>(c.D));
+        ws_bytes = pkv_decode_workspace_size(&desc, c.num_splits);
+        if (ws_bytes > 0) {
+            ws = dev_alloc<char>(ws_bytes);
+        }
+        desc.workspace = ws;
+        desc.workspace_bytes = ws_bytes;
+    }
+
+    void call(const KvSet& s, const int32_t* bt) const { call_entry(s, bt, entry); }
+
+    void call_entry(const KvSet& s, const int32_t* bt, const std::string& which) const {
+        if (which == "run_kernel") {
+            run_kernel(s.q, s.k, s.v, s.out, d_sl, bt, c.B, c.max_seqlen(), c.M, c.H, c.Hk, c.D, c.P, c.num_pages,
+                       c.causal ? 1 : 0);
+            const int st = pkv_last_status();
+            if (st != PKV_OK) {
+                die(std::string("run_kernel: ") + pkv_strerror(st));
+            }
+        } else {
+            const int st = pkv_decode(s.q, s.k, s.v, bt, d_sl, scale, c.num_splits, s.out, &desc, nullptr);
+            if (st != PKV_OK) {
+                die(std::string("pkv_decode: ") + pkv_strerror(st));
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ checks
+
+struct CheckResult {
+    bool ok = true;
+    bool finite = true;
+    int v_copy_rows = 0;
+    bool v_copy_exact = true;
+    int sampled = 0;
+    double max_abs_err = 0.0;
+    double tol = 0.0;
+    bool perm_identical = true;
+    bool entries_identical = true;
+    bool entries_compared = false;
+};
+
+// fp64 attention of output row (b, i, h) over the gathered keys it sees
+// (bottom-right causal when asked): the textbook softmax(q K^T scale) V.
+std::vector<double> attend_row(const Case& c, const std::vector<uint16_t>& q, const std::vector<uint16_t>& k,
+                               const std::vector<uint16_t>& v, int64_t b, int64_t i, int64_t h, double scale) {
+    const int64_t L = std::max(c.seqlens[static_cast<size_t>(b)], 0);
+    const int64_t last = c.causal ? std::min(L, i + L - c.M + 1) : L;
+    std::vector<double> o(static_cast<size_t>(c.D), 0.0);
+    if (last <= 0) {
+        return o;
+    }
+    const int64_t kvh = h / (c.H / c.Hk);
+    const uint16_t* qr = q.data() + ((b * c.M + i) * c.H + h) * c.D;
+    std::vector<double> s(static_cast<size_t>(last));
+    double mx = -INFINITY;
+    for (int64_t t = 0; t < last; ++t) {
+        const int64_t page = c.bt[static_cast<size_t>(b * c.stride + t / c.P)];
+        const uint16_t* kr = k.data() + ((page * c.P + t % c.P) * c.Hk + kvh) * c.D;
+        double dot = 0.0;
+        for (int64_t d = 0; d < c.D; ++d) {
+            dot += bits_to_double(qr[d], c.bf16) * bits_to_double(kr[d], c.bf16);
+        }
+        s[static_cast<size_t>(t)] = dot * scale;
+        mx = std::max(mx, s[static_cast<size_t>(t)]);
+    }
+    double den = 0.0;
+    for (int64_t t = 0; t < last; ++t) {
+        const double w = std::exp(s[static_cast<size_t>(t)] - mx);
+        den += w;
+        const int64_t page = c.bt[static_cast<size_t>(b * c.stride + t / c.P)];
+        const uint16_t* vr = v.data() + ((page * c.P + t % c.P) * c.Hk + kvh) * c.D;
+        for (int64_t d = 0; d < c.D; ++d) {
+            o[static_cast<size_t>(d)] += w * bits_to_double(vr[d], c.bf16);
+        }
+    }
+    for (double& x : o) {
+        x /= den;
+    }
+    return o;
+}
+
+CheckResult run_checks(const Case& c, const Runner& run, const KvSet& s, uint64_t seed) {
+    CheckResult r;
+    r.tol = c.bf16 ? 1e-2 : 2e-3;
+    const size_t out_n = static_cast<size_t>(c.B * c.M * c.H * c.D);
+    const size_t kv_n = static_cast<size_t>(c.num_pages * c.P * c.Hk * c.D);
+    run.call(s, run.d_bt);
+    hip_check(hipDeviceSynchronize(), "decode");
+    const std::vector<uint16_t> out = from_dev(s.out, out_n);
+    const std::vector<uint16_t> q = from_dev(s.q, out_n);
+    const std::vector<uint16_t> k = from_dev(s.k, kv_n);
+    const std::vector<uint16_t> v = from_dev(s.v, kv_n);
+
+    for (uint16_t x : out) {
+        r.finite = r.finite && std::isfinite(bits_to_double(x, c.bf16));
+    }
+    // One-token rows return that token's V row bit for bit to every query
+    // that sees it; with the causal mask query i of M sees key 0 only when
+    // i >= M - 1, and the earlier ones return zeros.
+    for (int64_t b = 0; b < c.B; ++b) {
+        if (c.seqlens[static_cast<size_t>(b)] != 1) {
+            continue;
+        }
+        ++r.v_copy_rows;
+        const int64_t page = c.bt[static_cast<size_t>(b * c.stride)];
+        for (int64_t i = 0; i < c.M; ++i) {
+            const bool sees = !c.causal || i >= c.M - 1;
+            for (int64_t h = 0; h < c.H; ++h) {
+                const uint16_t* want = v.data() + ((page * c.P) * c.Hk + h / (c.H / c.Hk)) * c.D;
+                const uint16_t* got = out.data() + ((b * c.M + i) * c.H + h) * c.D;
+                if (sees) {
+                    r.v_copy_exact = r.v_copy_exact && std::memcmp(want, got, static_cast<size_t>(c.D) * 2) == 0;
+                } else {
+                    for (int64_t d = 0; d < c.D; ++d) {
+                        r.v_copy_exact = r.v_copy_exact && bits_to_double(got[d], c.bf16) == 0.0;
+                    }
+                }
+            }
+        }
+    }
+    // fp64 attention on sampled rows: row 0, the longest row, and random ones.
+    Rng rng{seed ^ 0x5eedull};
+    std::vector<int64_t> rows = {0};
+    rows.push_back(std::max_element(c.seqlens.begin(), c.seqlens.end()) - c.seqlens.begin());
+    for (int k2 = 0; k2 < 30; ++k2) {
+        rows.push_back(rng.range(0, c.B - 1));
+    }
+    for (int64_t b : rows) {
+        const int64_t i = rng.range(0, c.M - 1);
+        const int64_t h = rng.range(0, c.H - 1);
+        const std::vector<double> want = attend_row(c, q, k, v, b, i, h, run.scale);
+        const uint16_t* got = out.data() + ((b * c.M + i) * c.H + h) * c.D;
+        for (int64_t d = 0; d < c.D; ++d) {
+            r.max_abs_err =
+                std::max(r.max_abs_err, std::fabs(bits_to_double(got[d], c.bf16) - want[static_cast<size_t>(d)]));
+        }
+        ++r.sampled;
+    }
+    // Moving every physical page (and block_table with it) changes no bit.
+    {
+        std::vector<int32_t> perm(static_cast<size_t>(c.num_pages));
+        for (int64_t p = 0; p < c.num_pages; ++p) {
+            perm[static_cast<size_t>(p)] = static_cast<int32_t>(p);
+        }
+        rng.shuffle(perm);
+        std::vector<int32_t> bt2(c.bt.size());
+        for (size_t j = 0; j < c.bt.size(); ++j) {
+            bt2[j] = perm[static_cast<size_t>(c.bt[j])];
+        }
+        int32_t* d_perm = dev_alloc<int32_t>(perm.size());
+        int32_t* d_bt2 = dev_alloc<int32_t>(bt2.size());
+        to_dev(d_perm, perm);
+        to_dev(d_bt2, bt2);
+        KvSet s2 = s;
+        s2.k = dev_alloc<uint16_t>(kv_n);
+        s2.v = dev_alloc<uint16_t>(kv_n);
+        s2.out = dev_alloc<uint16_t>(out_n);
+        const int64_t page_elems = c.P * c.Hk * c.D;
+        const int threads = 256;
+        const dim3 grid(static_cast<unsigned>(blocks_for(c.num_pages * page_elems, threads)));
+        permute_pages_kernel<<<grid, dim3(threads)>>>(s.k, s2.k, d_perm, c.num_pages, page_elems);
+        permute_pages_kernel<<<grid, dim3(threads)>>>(s.v, s2.v, d_perm, c.num_pages, page_elems);
+        hip_check(hipGetLastError(), "permute kernel");
+        run.call(s2, d_bt2);
+        hip_check(hipDeviceSynchronize(), "decode (permuted pages)");
+        r.perm_identical = from_dev(s2.out, out_n) == out;
+        // The reference's 15-argument entry and pkv_decode with its defaults
+        // (bf16, scale 1/sqrt(D), heuristic splits, block_table rows of
+        // num_pages / B entries) give the same bits.
+        if (legacy_entry_fits(c)) {
+            r.entries_compared = true;
+            KvSet s3 = s;
+            s3.out = s2.out;
+            run.call_entry(s3, run.d_bt, run.entry == "run_kernel" ? "pkv_decode" : "run_kernel");
+            hip_check(hipDeviceSynchronize(), "decode (other entry)");
+            r.entries_identical = from_dev(s2.out, out_n) == out;
+        }
+        hip_check(hipFree(s2.k), "hipFree");
+        hip_check(hipFree(s2.v), "hipFree");
+        hip_check(hipFree(s2.out), "hipFree");
+        hip_check(hipFree(d_perm), "hipFree");
+        hip_check(hipFree(d_bt2), "hipFree");
+    }
+    r.ok = r.finite && r.v_copy_exact && r.max_abs_err <= r.tol && r.perm_identical && r.entries_identical;
+    return r;
+}
+
+// ------------------------------------------------------------------ main
+
+std::vector<int64_t> parse_list(const std::string& s) {
+    std::vector<int64_t> v;
+    size_t pos = 0;
+    while (pos <= s.size()) {
+        const size_t comma = s.find(',', pos);
+        const std::string tok = s.substr(pos, comma == std::string::npos ? std::string::npos : comma - pos);
+        char* end = nullptr;
+        const long long x = std::strtoll(tok.c_str(), &end, 10);
+        if (tok.empty() || *end != '\0') {
+            die("bad number in --case: " + tok);
+        }
+        v.push_back(x);
+        if (comma == std::string::npos) {
+            break;
+        }
+        pos = comma + 1;
+    }
+    return v;
+}
+
+void usage() {
+    std::printf(
+        "usage: pkv_harness (--config c1..c5 | --case B,S,M,H,Hk,D,P [--profile legacy|contest])\n"
+        "                   [--entry pkv_decode|run_kernel] [--dtype bf16|f16] [--splits N] [--causal]\n"
+        "                   [--warmup W] [--repeat R] [--sets N] [--seed S] [--check]\n");
+}
+
+} // namespace
+
+int main(int argc, char** argv) {
+    std::string config, case_spec, profile = "legacy", entry = "pkv_decode", dtype;
+    int splits = -1, warmup = 20, repeat = 100, sets = 3;
+    bool check = false, causal = false;
+    uint64_t seed = 1001;
+    for (int a = 1; a < argc; ++a) {
+        const std::string arg = argv[a];
+        auto value = [&]() -> std::string {
+            if (a + 1 >= argc) {
+                die("missing value after " + arg);
+            }
+            return argv[++a];
+        };
+        if (arg == "--help" || arg == "-h") {
+            usage();
+            return 0;
+        } else if (arg == "--config") {
+            config = value();
+        } else if (arg == "--case") {
+            case_spec = value();
+        } else if (arg == "--profile") {
+            profile = value();
+        } else if (arg == "--entry") {
+            entry = value();
+        } else if (arg == "--dtype") {
+            dtype = value();
+        } else if (arg == "--splits") {
+            splits = std::atoi(value().c_str());
+        } else if (arg == "--warmup") {
+            warmup = std::atoi(value().c_str());
+        } else if (arg == "--repeat") {
+            repeat = std::atoi(value().c_str());
+        } else if (arg == "--sets") {
+            sets = std::atoi(value().c_str());
+        } else if (arg == "--seed") {
+            seed = std::strtoull(value().c_str(), nullptr, 10);
+        } else if (arg == "--check") {
+            check = true;
+        } else if (arg == "--causal") {
+            causal = true;
+        } else {
+            usage();
+            die("unknown argument " + arg);
+        }
+    }
+    if (config.empty() == case_spec.empty()) {
+        usage();
+        die("give exactly one of --config and --case");
+    }
+    if (entry != "pkv_decode" && entry != "run_kernel") {
+        die("--entry is pkv_decode or run_kernel");
+    }
+    if (profile != "legacy" && profile != "contest") {
+        die("--profile is legacy or contest");
+    }
+    if (warmup < 0 || repeat < 1 || sets < 1) {
+        die("--warmup >= 0, --repeat >= 1, --sets >= 1");
+    }
+
+    Case c;
+    if (!config.empty()) {
+        c = make_config(config, seed);
+    } else {
+        const std::vector<int64_t> v = parse_list(case_spec);
+        if (v.size() != 7 || *std::min_element(v.begin(), v.end()) < 1) {
+            die("--case takes seven positive numbers B,S,M,H,Hk,D,P");
+        }
+        c = make_eval_case(v[0], v[1], v[2], v[3], v[4], v[5], v[6], profile == "contest", seed);
+    }
+    if (!dtype.empty()) {
+        if (dtype != "bf16" && dtype != "f16") {
+            die("--dtype is bf16 or f16");
+        }
+        c.bf16 = dtype == "bf16";
+    }
+    if (splits >= 0) {
+        c.num_splits = splits;
+    }
+    c.causal = causal;
+    if (entry == "run_kernel" && !legacy_entry_fits(c)) {
+        die("run_kernel is the reference's bf16 entry with heuristic splits and block_table rows of "
+            "num_pages / B entries: use --case with --dtype bf16 and no --splits");
+    }
+    if (c.H % c.Hk != 0) {
+        die("H must be a multiple of Hk");
+    }
+
+    int devices = 0;
+    hip_check(hipGetDeviceCount(&devices), "hipGetDeviceCount");
+    if (devices < 1) {
+        die("no GPU");
+    }
+    Runner run(c, entry);
+    const size_t kv_n = static_cast<size_t>(c.num_pages * c.P * c.Hk * c.D);
+    const size_t out_n = static_cast<size_t>(c.B * c.M * c.H * c.D);
+    std::vector<KvSet> kv(static_cast<size_t>(sets));
+    for (int i = 0; i < sets; ++i) {
+        KvSet& s = kv[static_cast<size_t>(i)];
+        s.k = dev_alloc<uint16_t>(kv_n);
+        s.v = dev_alloc<uint16_t>(kv_n);
+        s.q = dev_alloc<uint16_t>(out_n);
+        s.out = dev_alloc<uint16_t>(out_n);
+        const uint64_t sd = seed * 1315423911ull + 7919ull * static_cast<uint64_t>(i);
+        fill(s.k, static_cast<int64_t>(kv_n), static_cast<int>(c.D), sd + 1, c.kv_sigma, c.k_peak_prob, c.bf16);
+        fill(s.v, static_cast<int64_t>(kv_n), static_cast<int>(c.D), sd + 2, c.kv_sigma, 0.f, c.bf16);
+        fill(s.q, static_cast<int64_t>(out_n), static_cast<int>(c.D), sd + 3, c.q_sigma, 0.f, c.bf16);
+    }
+    hip_check(hipDeviceSynchronize(), "fill");
+
+    CheckResult cr;
+    if (check) {
+        cr = run_checks(c, run, kv[0], seed);
+    }
+
+    // time_cuda: warm-up calls, then `repeat` calls between two events,
+    // rotating over the K/V sets so no call finds its pages in the caches.
+    for (int i = 0; i < warmup; ++i) {
+        run.call(kv[static_cast<size_t>(i % sets)], run.d_bt);
+    }
+    hip_check(hipDeviceSynchronize(), "warm-up");
+    hipEvent_t e0, e1;
+    hip_check(hipEventCreate(&e0), "hipEventCreate");
+    hip_check(hipEventCreate(&e1), "hipEventCreate");
+    hip_check(hipEventRecord(e0, nullptr), "hipEventRecord");
+    for (int i = 0; i < repeat; ++i) {
+        run.call(kv[static_cast<size_t>(i % sets)], run.d_bt);
+    }
+    hip_check(hipEventRecord(e1, nullptr), "hipEventRecord");
+    hip_check(hipEventSynchronize(e1), "hipEventSynchronize");
+    float ms = 0.f;
+    hip_check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    const double us = 1e3 * ms / repeat;
+    const double gbps = static_cast<double>(c.kv_bytes()) / (us * 1e-6) / 1e9;
+
+    int64_t total_len = 0;
+    for (int32_t s : c.seqlens) {
+        total_len += s;
+    }
+    std::printf(
+        "{\"harness\": \"pkv_harness\", \"entry\": \"%s\", \"case\": {\"name\": \"%s\", \"batch\": %lld, "
+        "\"seqlen_q\": %lld, \"num_heads\": %lld, \"num_heads_k\": %lld, \"head_dim\": %lld, \"page_size\": %lld, "
+        "\"num_pages\": %lld, \"dtype\": \"%s\", \"causal\": %s, \"num_splits\": %d, \"seqlen_sum\": %lld, "
+        "\"seqlen_max\": %lld, \"seed\": %llu}, \"schedule\": %d, \"workers\": %d, \"sets\": %d, \"warmup\": %d, "
+        "\"repeat\": %d, \"us_per_call\": %.3f, \"kv_gbps\": %.1f, \"hbm_frac_kv\": %.4f",
+        entry.c_str(), c.name.c_str(), static_cast<long long>(c.B), static_cast<long long>(c.M),
+        static_cast<long long>(c.H), static_cast<long long>(c.Hk), static_cast<long long>(c.D),
+        static_cast<long long>(c.P), static_cast<long long>(c.num_pages), c.bf16 ? "bf16" : "f16",
+        c.causal ? "true" : "false", c.num_splits, static_cast<long long>(total_len),
+        static_cast<long long>(c.max_seqlen()), static_cast<unsigned long long>(seed),
+        pkv_decode_schedule(&run.desc, c.num_splits), pkv_decode_num_splits(&run.desc, c.num_splits), sets, warmup,
+        repeat, us, gbps, gbps / 8000.0);
+    if (check) {
+        std::printf(
+            ", \"check\": {\"ok\": %s, \"finite\": %s, \"v_copy_rows\": %d, \"v_copy_exact\": %s, "
+            "\"sampled_rows\": %d, \"max_abs_err\": %.3g, \"tol\": %g, \"permuted_pages_identical\": %s, "
+            "\"entries_identical\": %s}",
+            cr.ok ? "true" : "false", cr.finite ? "true" : "false", cr.v_copy_rows, cr.v_copy_exact ? "true" : "false",
+            cr.sampled, cr.max_abs_err, cr.tol, cr.perm_identical ? "true" : "false",
+            cr.entries_compared ? (cr.entries_identical ? "true" : "false") : "null");
+    }
+    std::printf("}\n");
+    return check && !cr.ok ? 1 : 0;
+}

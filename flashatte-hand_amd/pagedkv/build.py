@@ -1,7 +1,8 @@
 """Build recipe for the gfx950 library ``libpkv_decode.so`` and the CPU oracle.
 
 The HIP sources are compiled with hipcc for gfx950 only, one object per source
-(in parallel), then linked into ``flashatte-hand_amd/lib/libpkv_decode.so``.
+(in parallel), then linked into ``flashatte-hand_amd/lib/libpkv_decode.so``;
+the C++ host harness ``flashatte-hand_amd/lib/pkv_harness`` links against it.
 Packed-fp32 VALU instructions are disabled for all device code
 (``-packed-fp32-ops``).  The oracle (test infrastructure) is built with its own
 Makefile into ``oracle/libpkv_oracle.so``.
@@ -20,6 +21,7 @@ CSRC = PKG_ROOT / "csrc"
 BUILD_DIR = PKG_ROOT / "_build"
 LIB_DIR = PKG_ROOT / "lib"
 LIB_PATH = LIB_DIR / "libpkv_decode.so"
+HARNESS_SRC = PKG_ROOT / "harness" / "pkv_harness.hip"
 ORACLE_DIR = REPO_ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "libpkv_oracle.so"
 
@@ -85,6 +87,19 @@ def build_library(verbose: bool = False, jobs: int = 0, out: Path | None = None,
     return lib_path
 
 
+def build_harness(verbose: bool = False, lib_path: Path | None = None) -> Path:
+    """Compile the C++ host harness (harness/pkv_harness.hip) next to the library it links."""
+    lib_path = Path(lib_path) if lib_path else LIB_PATH
+    if not lib_path.exists():
+        raise RuntimeError(f"{lib_path} is not built; build_library() first")
+    exe = lib_path.parent / "pkv_harness"
+    tmp = exe.with_name(exe.name + ".tmp")
+    _run([_hipcc(), *HIPCC_FLAGS, "-x", "hip", str(HARNESS_SRC), "-o", str(tmp),
+          f"-L{lib_path.parent}", "-l" + lib_path.stem[3:], "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, exe)
+    return exe
+
+
 def build_oracle(verbose: bool = False) -> Path:
     """Build the CPU oracle (test infrastructure) with its Makefile."""
     cmd = ["make", "-s", "-B", "-C", str(ORACLE_DIR)]
@@ -97,4 +112,5 @@ if __name__ == "__main__":
 
     v = "-v" in sys.argv
     print(build_library(verbose=v))
+    print(build_harness(verbose=v))
     print(build_oracle(verbose=v))
