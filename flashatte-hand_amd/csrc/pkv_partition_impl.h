@@ -113,9 +113,10 @@ __device__ __forceinline__ typename TileRegs<64, FP8>::Chunk load_chunk(const ch
 // is read from the page window with readlane; otherwise each lane fetches its
 // own token's page id from the window with ds_bpermute.  Neither waits on a
 // global load, so earlier tiles' loads stay in flight.  When `real` is false
-// (a prefetch past the end of the range) every lane loads the same line at the
-// start of the caches instead: the loop then issues the same number of loads
-// on every path, which keeps the compiler's wait counts exact.  (Buffer loads
+// (a prefetch past the end of the range) the loads still go out, to lines
+// already read (WIDE: token end - 1's row) or to the start of the caches: the
+// loop then issues the same number of loads on every path, which keeps the
+// compiler's wait counts exact.  (Buffer loads
 // through a per-tile descriptor — one 32-bit offset per lane, rows past the
 // range read as zeros — cut the loop's VALU from 86 to 67 per tile but
 // measured 1-4 % slower.)
@@ -132,18 +133,24 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
     const uint32_t col = static_cast<uint32_t>((kvh * D + 8 * (lane % L)) * EB); // bytes within a token row
     const uint32_t ts2 = static_cast<uint32_t>(p.token_stride) * EB;            // bytes per token
     if constexpr (WIDE) {
-        // Wave-uniform page base (SGPRs) + 32-bit lane offsets.
-        const int idx = real ? (t0 >> p.page_shift) - win_base : 0;
-        const int phys = __builtin_amdgcn_readlane(win, idx);
-        const int64_t base =
-            real ? (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(t0 & pmask) * p.token_stride) * EB
-                 : 0;
+        // Wave-uniform page base in SGPRs (so the loads take the SGPR-base +
+        // 32-bit-offset form) and per-lane offsets that are loop invariant
+        // except for one clamp: a lane's token is min(R i + rl, lim), and as
+        // offsets grow with the token the clamp is a min on the byte offset.
+        // A prefetch past the range reads the row of token end - 1 on every
+        // lane: the last real tile has just loaded it, and the window holds
+        // its page.
+        const bool live = uniform(real ? 1 : 0) != 0;
+        const int ts = uniform(live ? t0 : end - 1);
+        const int phys = __builtin_amdgcn_readlane(win, (ts >> p.page_shift) - win_base);
+        const int64_t base = uniform(
+            (static_cast<int64_t>(phys) * p.page_stride + static_cast<int64_t>(ts & pmask) * p.token_stride) * EB);
         const char* kb = reinterpret_cast<const char*>(p.k) + base;
         const char* vb = reinterpret_cast<const char*>(p.v) + base;
-        const int lim = real ? end - 1 - t0 : 0; // clamp: never touch unowned slots
+        const uint32_t lim_off = static_cast<uint32_t>(uniform(live ? end - 1 - t0 : 0)) * ts2 + col;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const uint32_t off = real ? static_cast<uint32_t>(min(R * i + rl, lim)) * ts2 + col : 0u;
+            const uint32_t off = min(static_cast<uint32_t>(R * i + rl) * ts2 + col, lim_off);
             r.k[i] = load_chunk<FP8>(kb + off);
             r.v[i] = load_chunk<FP8>(vb + off);
         }
