@@ -350,6 +350,9 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         const int64_t parts_est = plan.splits / std::max<int64_t>(streams, 1) + 1;
         const int64_t stream_waves = streams * ((p.part_heads + pkv::kStreamRows - 1) / pkv::kStreamRows);
         c.by_stream = tiles && stream_waves >= 8 * kComputeUnits && parts_est <= 1024 / r.D ? 1 : 0;
+        // More than 16 parts per stream (long rows, few streams: C3 has 13-52):
+        // the row-per-wave combine keeps all of them in flight at once.
+        c.long_rows = tiles && !c.by_stream && parts_est > 16 ? 1 : 0;
         c.num_heads = static_cast<int32_t>(r.H);
         c.splits = splits;
         c.split_tokens = plan.split_tokens;

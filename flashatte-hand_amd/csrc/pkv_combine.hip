@@ -174,11 +174,12 @@ __device__ __forceinline__ RowUnits row_units(const CombineParams& p, int32_t b,
 // partition's unit arithmetic.  One worker means the partition already wrote
 // the row; a row without tokens gets zeros; otherwise the partials in slots
 // w_a + r .. w_b + r are merged with their LSEs, kBatch partial rows in flight
-// at a time.
-template <bool BF16, int D>
+// at a time: 16, or for streams of many parts (long rows) as many as 128
+// registers hold, so such a row takes one round trip instead of several.
+template <bool BF16, int D, int kBatch>
 __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
-    constexpr int kBatch = 16;
+    static_assert(kBatch <= 64 && 64 % kBatch == 0, "a batch of parts takes its weights from one LSE lane each");
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= p.rows) {
@@ -473,8 +474,11 @@ static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, c
         const int waves = p.batch * spr * ((p.part_heads + kStreamRows - 1) / kStreamRows);
         launch_kernel(combine_streams_kernel<BF16, D>, dim3((waves + kWaves - 1) / kWaves), dim3(64 * kWaves), 0,
                       stream, ev, p);
+    } else if (p.tile_workers > 0 && p.long_rows) {
+        constexpr int kLong = 128 / (D / 64) < 64 ? 128 / (D / 64) : 64;
+        launch_kernel(combine_tiles_kernel<BF16, D, kLong>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else if (p.tile_workers > 0) {
-        launch_kernel(combine_tiles_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
+        launch_kernel(combine_tiles_kernel<BF16, D, 16>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else {
         launch_kernel(combine_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     }
