@@ -13,6 +13,8 @@ Two call surfaces over the C ABI of ``libpkv_decode.so``:
 and the paged KV-cache append that precedes a decode step: ``k`` / ``v`` of
 :func:`flash_attn_with_kvcache` (flash-attn 2.6.3 semantics), :func:`append_kv`
 (block-table positions) and :func:`reshape_and_cache_flash` (flat slots).
+:func:`torch_binding` returns the compiled torch extension over the same library
+(the reference's binding ``run_kernel`` and a stream-aware ``decode``).
 
 Both run the gfx950 HIP kernels; there is no CPU or PyTorch fallback.  Torch
 is used only to hand over device pointers and the current HIP stream.
@@ -476,3 +478,30 @@ def run_kernel(
     st = lib.pkv_last_status()
     if st != PKV_OK:
         raise PkvError(st, "run_kernel")
+
+
+_TORCH_BINDING = None
+
+
+def torch_binding():
+    """The compiled torch extension ``lib/pkv_torch*.so`` (source ``binding/pkv_torch.cpp``): the
+    reference's binding ``run_kernel`` (eval:24-86, tensors + the 15 arguments) and
+    ``decode(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale=0, num_splits=0,
+    causal=False, max_seqlen=0) -> out`` on torch's current stream, both over libpkv_decode.so.
+    Raises if it has not been built (pagedkv.build.build_torch_binding)."""
+    global _TORCH_BINDING
+    if _TORCH_BINDING is None:
+        import importlib.machinery
+        import importlib.util
+
+        _torch()  # the extension resolves torch's libraries from the loaded process
+        lib_dir = _lib.LIB_PATH.parent
+        found = sorted(lib_dir.glob("pkv_torch*.so"))
+        if not found:
+            raise ImportError(f"no pkv_torch*.so in {lib_dir}; build it with pagedkv.build.build_torch_binding()")
+        loader = importlib.machinery.ExtensionFileLoader("pkv_torch", str(found[0]))
+        spec = importlib.util.spec_from_loader("pkv_torch", loader)
+        module = importlib.util.module_from_spec(spec)
+        loader.exec_module(module)
+        _TORCH_BINDING = module
+    return _TORCH_BINDING

@@ -2,7 +2,8 @@
 
 The HIP sources are compiled with hipcc for gfx950 only, one object per source
 (in parallel), then linked into ``flashatte-hand_amd/lib/libpkv_decode.so``;
-the C++ host harness ``flashatte-hand_amd/lib/pkv_harness`` links against it.
+the C++ host harness ``flashatte-hand_amd/lib/pkv_harness`` and the torch extension
+``flashatte-hand_amd/lib/pkv_torch.so`` link against it.
 Packed-fp32 VALU instructions are disabled for all device code
 (``-packed-fp32-ops``).  The oracle (test infrastructure) is built with its own
 Makefile into ``oracle/libpkv_oracle.so``.
@@ -22,6 +23,8 @@ BUILD_DIR = PKG_ROOT / "_build"
 LIB_DIR = PKG_ROOT / "lib"
 LIB_PATH = LIB_DIR / "libpkv_decode.so"
 HARNESS_SRC = PKG_ROOT / "harness" / "pkv_harness.hip"
+TORCH_BINDING = "pkv_torch"
+TORCH_BINDING_SRC = PKG_ROOT / "binding" / "pkv_torch.cpp"
 ORACLE_DIR = REPO_ROOT / "oracle"
 ORACLE_LIB = ORACLE_DIR / "libpkv_oracle.so"
 
@@ -100,6 +103,31 @@ def build_harness(verbose: bool = False, lib_path: Path | None = None) -> Path:
     return exe
 
 
+def build_torch_binding(verbose: bool = False) -> Path:
+    """Compile the torch extension binding/pkv_torch.cpp (the reference's run_kernel binding and a
+    stream-aware decode) against libpkv_decode.so, and place it next to the library as
+    lib/pkv_torch*.so, importable with pagedkv.torch_binding()."""
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is not built; build_library() first")
+    from torch.utils import cpp_extension
+
+    os.environ.setdefault("PYTORCH_ROCM_ARCH", "gfx950")
+    build_dir = BUILD_DIR / "torch_binding"
+    build_dir.mkdir(parents=True, exist_ok=True)
+    # Loaded from the build folder right after building, and from lib/ afterwards.
+    cpp_extension.load(name=TORCH_BINDING, sources=[str(TORCH_BINDING_SRC)],
+                       extra_include_paths=[str(REPO_ROOT / "include")], extra_cflags=["-O2"],
+                       # $ORIGIN escaped for ninja ($$) and for the shell it runs (\\$)
+                       extra_ldflags=[f"-L{LIB_DIR}", "-lpkv_decode", "-Wl,-rpath,\\$$ORIGIN:\\$$ORIGIN/../../lib"],
+                       build_directory=str(build_dir), with_cuda=True, verbose=verbose)
+    built = build_dir / f"{TORCH_BINDING}.so"
+    dest = LIB_DIR / built.name
+    tmp = dest.with_name(dest.name + ".tmp")
+    shutil.copyfile(built, tmp)
+    os.replace(tmp, dest)
+    return dest
+
+
 def build_oracle(verbose: bool = False) -> Path:
     """Build the CPU oracle (test infrastructure) with its Makefile."""
     cmd = ["make", "-s", "-B", "-C", str(ORACLE_DIR)]
@@ -113,4 +141,5 @@ if __name__ == "__main__":
     v = "-v" in sys.argv
     print(build_library(verbose=v))
     print(build_harness(verbose=v))
+    print(build_torch_binding(verbose=v))
     print(build_oracle(verbose=v))
