@@ -113,7 +113,9 @@ def build_torch_binding(verbose: bool = False) -> Path:
 
     os.environ.setdefault("PYTORCH_ROCM_ARCH", "gfx950")
     build_dir = BUILD_DIR / "torch_binding"
-    build_dir.mkdir(parents=True, exist_ok=True)
+    if build_dir.exists():
+        shutil.rmtree(build_dir)  # always compile (the build check), not ninja's incremental rebuild
+    build_dir.mkdir(parents=True)
     # Loaded from the build folder right after building, and from lib/ afterwards.
     cpp_extension.load(name=TORCH_BINDING, sources=[str(TORCH_BINDING_SRC)],
                        extra_include_paths=[str(REPO_ROOT / "include")], extra_cflags=["-O2"],
