@@ -12,6 +12,10 @@ shares no code with the C oracle or the HIP kernels:
 262-272; layout: scripts/evaluate_flashattn_submission.py:127-143).  The
 "select" case is a closed form instead: each query head scores one chosen token
 2^6 higher than all others, so its output is that token's V row exactly.
+The `mask_*` fixtures write out flash-attn 2.6.3's masks for several query tokens
+(the arguments at eval:242-245), the `fp8_*` ones decode E4M3 from its bit fields
+and quantise by nearest-code table search, and the `append_*` ones place the new
+tokens by slot arithmetic — none of it shared with the oracle or the kernels.
 
 The reference holds no vectors of its own (its only check is against flash_attn
 on a MetaX GPU), so these fixtures are the repository's frozen anchors.
@@ -136,6 +140,156 @@ def select_case(dtype):
                 dtype=dtype, expected=expected, exact=np.bool_(True))
 
 
+# ---------------------------------------------------------------- several query tokens, masks, ALiBi
+
+def mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, alibi, kf=None, vf=None):
+    """flash-attn 2.6.3 semantics, written out directly: query i of M sits at position
+    pos = i + L - M and sees the keys j < L with pos - left <= j <= pos + right (-1 = unbounded;
+    causal makes right 0); ALiBi subtracts slope * |pos - j| from the scaled score; a query that
+    sees no key returns 0.  kf / vf: dequantised caches (FP8 cases)."""
+    qf = from_bits(q, dtype)
+    kf = from_bits(k, dtype) if kf is None else kf
+    vf = from_bits(v, dtype) if vf is None else vf
+    B, M, H, D = q.shape
+    P, Hk = kf.shape[1], kf.shape[2]
+    G = H // Hk
+    left, right = window
+    if causal:
+        right = 0
+    out = np.zeros((B, M, H, D))
+    for b in range(B):
+        L = int(seqlens[b])
+        for i in range(M):
+            pos = i + L - M
+            lo = 0 if left < 0 else max(0, pos - left)
+            hi = L - 1 if right < 0 else min(L - 1, pos + right)
+            if L <= 0 or hi < lo:
+                continue
+            t = np.arange(lo, hi + 1)
+            pages = bt[b, t // P]
+            for h in range(H):
+                kk = kf[pages, t % P, h // G]
+                vv = vf[pages, t % P, h // G]
+                s = kk @ qf[b, i, h] * scale
+                if alibi is not None:
+                    slope = alibi[b, h] if alibi.ndim == 2 else alibi[h]
+                    s = s - float(slope) * np.abs(pos - t)
+                p = np.exp(s - s.max())
+                out[b, i, h] = (p / p.sum()) @ vv
+    return out
+
+
+def mask_case(name, seed, B, H, Hk, D, P, seqlens, dtype, M, causal, window=(-1, -1), alibi=None):
+    rng = np.random.default_rng(seed)
+    seqlens = np.asarray(seqlens, dtype=np.int32)
+    pages = (np.maximum(seqlens, 0) + P - 1) // P
+    pool = int(pages.sum()) + 2
+    bt = scattered_table(rng, seqlens, P, pool, max(1, int(pages.max())))
+    q = to_bits(rng.standard_normal((B, M, H, D)), dtype)
+    k = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+    v = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+    slopes = None
+    if alibi == "H":
+        slopes = rng.uniform(0.02, 0.3, H).astype(np.float32)
+    elif alibi == "BH":
+        slopes = rng.uniform(0.02, 0.3, (B, H)).astype(np.float32)
+    scale = 1.0 / np.sqrt(D)
+    c = dict(name=name, q=q, k=k, v=v, block_table=bt, seqlens=seqlens, scale=np.float64(scale), dtype=dtype,
+             causal=np.bool_(causal), window=np.array(window, dtype=np.int32),
+             expected=mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, slopes))
+    if slopes is not None:
+        c["alibi"] = slopes
+    return c
+
+
+# ---------------------------------------------------------------- OCP FP8 e4m3 caches
+
+def e4m3_value(code):
+    """OCP E4M3 decoded from its bit fields: bias 7, subnormals at exponent 0, no infinities,
+    0x7f / 0xff NaN."""
+    code = np.asarray(code, dtype=np.int64)
+    sign = np.where(code >> 7, -1.0, 1.0)
+    e = (code >> 3) & 15
+    m = code & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    mag = np.where((e == 15) & (m == 7), np.nan, mag)
+    return sign * mag
+
+
+MAG_CODES = np.arange(0x7F, dtype=np.int64)          # the 127 finite non-negative codes, 0 .. 448
+MAG_VALUES = e4m3_value(MAG_CODES)
+
+
+def e4m3_encode(x):
+    """Sign and magnitude: the magnitude goes to the nearest finite code by table search (ties to
+    the even code, saturating at 448), the sign bit is copied, so values that round to zero keep
+    their sign."""
+    x = np.asarray(x, dtype=np.float64)
+    mag = np.minimum(np.abs(x), 448.0)
+    d = np.abs(mag[..., None] - MAG_VALUES)
+    best = d.min(axis=-1, keepdims=True)
+    cand = np.where(d == best, MAG_CODES, 1 << 20)
+    even = np.where((cand & 1) == 0, cand, 1 << 20)
+    code = np.where(even.min(axis=-1) < (1 << 20), even.min(axis=-1), cand.min(axis=-1))
+    return (code | np.where(np.signbit(x), 0x80, 0)).astype(np.uint8)
+
+
+def fp8_case(name, seed, B, H, Hk, D, P, seqlens, dtype, M=1, causal=False):
+    rng = np.random.default_rng(seed)
+    seqlens = np.asarray(seqlens, dtype=np.int32)
+    pages = (np.maximum(seqlens, 0) + P - 1) // P
+    pool = int(pages.sum()) + 2
+    bt = scattered_table(rng, seqlens, P, pool, max(1, int(pages.max())))
+    q = to_bits(rng.standard_normal((B, M, H, D)), dtype)
+    ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+    vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+    k8 = e4m3_encode(rng.standard_normal((pool, P, Hk, D)) / ks[:, None])
+    v8 = e4m3_encode(rng.standard_normal((pool, P, Hk, D)) / vs[:, None])
+    kf = e4m3_value(k8) * ks[:, None].astype(np.float64)
+    vf = e4m3_value(v8) * vs[:, None].astype(np.float64)
+    scale = 1.0 / np.sqrt(D)
+    return dict(name=name, q=q, k8=k8, v8=v8, k_scale=ks, v_scale=vs, block_table=bt, seqlens=seqlens,
+                scale=np.float64(scale), dtype=dtype, causal=np.bool_(causal),
+                expected=mask_expected(q, None, None, bt, seqlens, scale, dtype, causal, (-1, -1), None, kf, vf))
+
+
+# ---------------------------------------------------------------- paged KV-cache append
+
+def append_case(name, seed, B, Hk, D, P, lens, n, dtype, fp8=False):
+    """Cache contents after writing token j of row b at position lens[b] + j, i.e. page
+    block_table[b, pos // P], slot pos % P (flash-attn 2.6.3 k= / v=)."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int32)
+    pages = (lens + n + P - 1) // P
+    pool = int(pages.sum()) + 2
+    bt = scattered_table(rng, lens + n, P, pool, int(pages.max()))
+    nk = to_bits(rng.standard_normal((B, n, Hk, D)) * 2.0, dtype)
+    nv = to_bits(rng.standard_normal((B, n, Hk, D)) * 2.0, dtype)
+    c = dict(name=name, block_table=bt, seqlens=lens, k_new=nk, v_new=nv, dtype=dtype)
+    if fp8:
+        ks = rng.uniform(0.3, 3.0, Hk).astype(np.float32)
+        vs = rng.uniform(0.3, 3.0, Hk).astype(np.float32)
+        kc = e4m3_encode(rng.standard_normal((pool, P, Hk, D)))
+        vc = e4m3_encode(rng.standard_normal((pool, P, Hk, D)))
+        # the quantiser: x * (1 / scale) in fp32, then to e4m3
+        qk = e4m3_encode(from_bits(nk, dtype).astype(np.float32) * (np.float32(1) / ks)[:, None])
+        qv = e4m3_encode(from_bits(nv, dtype).astype(np.float32) * (np.float32(1) / vs)[:, None])
+        c.update(k_scale=ks, v_scale=vs)
+    else:
+        kc = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+        vc = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+        qk, qv = nk, nv
+    ek, ev = kc.copy(), vc.copy()
+    for b in range(B):
+        for j in range(n):
+            pos = int(lens[b]) + j
+            page = bt[b, pos // P]
+            ek[page, pos % P] = qk[b, j]
+            ev[page, pos % P] = qv[b, j]
+    c.update(k_cache=kc, v_cache=vc, expected_k=ek, expected_v=ev)
+    return c
+
+
 def main():
     cases = [
         c1_case(),
@@ -145,6 +299,17 @@ def main():
         random_case("group48_p8", 104, B=1, H=48, Hk=1, D=128, P=8, seqlens=[70], dtype="f16"),
         select_case("bf16"),
         select_case("f16"),
+        mask_case("mask_causal_m4_bf16", 201, B=3, H=16, Hk=4, D=128, P=16, seqlens=[2, 50, 300], dtype="bf16",
+                  M=4, causal=True),
+        mask_case("mask_window_alibi_f16", 202, B=2, H=8, Hk=2, D=64, P=32, seqlens=[100, 257], dtype="f16", M=3,
+                  causal=False, window=(40, 5), alibi="BH"),
+        mask_case("mask_sliding_alibi_bf16", 203, B=2, H=8, Hk=2, D=128, P=64, seqlens=[1000, 37], dtype="bf16",
+                  M=1, causal=False, window=(128, -1), alibi="H"),
+        fp8_case("fp8_bf16_d128", 301, B=3, H=32, Hk=8, D=128, P=16, seqlens=[1, 64, 500], dtype="bf16"),
+        fp8_case("fp8_f16_causal_d64", 302, B=2, H=8, Hk=2, D=64, P=32, seqlens=[40, 130], dtype="f16", M=2,
+                 causal=True),
+        append_case("append_bf16", 401, B=4, Hk=2, D=128, P=16, lens=[0, 15, 16, 70], n=3, dtype="bf16"),
+        append_case("append_fp8_f16", 402, B=3, Hk=2, D=64, P=8, lens=[0, 7, 33], n=2, dtype="f16", fp8=True),
     ]
     for c in cases:
         name = c.pop("name")

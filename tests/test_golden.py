@@ -1,9 +1,14 @@
 """Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
 
-CPU: the oracle reproduces every fixture's expected output (fp64 dense formula
-computed independently at fixture time; closed form for the select cases).
-GPU: the HIP path, through the C ABI, matches every fixture within the north-star
-tolerance on every schedule, and the select cases bit for bit.
+Kinds: one-token decode over 16-bit caches (the unprefixed names), several query tokens with
+causal / window / ALiBi masks (`mask_*`), OCP FP8 e4m3 caches with per-head scales (`fp8_*`),
+and the paged append (`append_*`, 16-bit and FP8).
+CPU: the oracle reproduces every fixture's expected output (fp64 dense formulas and
+slot arithmetic computed independently at fixture time; closed form for the select cases),
+and the fixtures' table-search E4M3 encoder agrees with the oracle's quantiser.
+GPU: the HIP path, through the C ABI, matches every decode fixture within the north-star
+tolerance on every schedule (the select cases bit for bit; masked and FP8 ones also allow the
+output's own rounding, half an ulp), and the append fixtures bit for bit.
 """
 from __future__ import annotations
 
@@ -16,21 +21,76 @@ import pkv_oracle as po
 from conftest import gpu_available
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-FIXTURES = sorted(p.stem for p in GOLDEN.glob("*.npz"))
+ALL = sorted(p.stem for p in GOLDEN.glob("*.npz"))
+MASK = [n for n in ALL if n.startswith("mask_")]
+FP8 = [n for n in ALL if n.startswith("fp8_")]
+APPEND = [n for n in ALL if n.startswith("append_")]
+FIXTURES = [n for n in ALL if n not in MASK + FP8 + APPEND]  # one query token, 16-bit caches
 TOL = {0: 2e-3, 1: 1e-2}
+REL = {0: 2.0 ** -11, 1: 2.0 ** -8}  # half an ulp of the output dtype (its own rounding)
 
 
 def load(name):
     z = np.load(GOLDEN / f"{name}.npz", allow_pickle=False)
     d = {k: z[k] for k in z.files}
     d["dtype_code"] = 0 if str(d["dtype"]) == "f16" else 1
-    d["scale"] = float(d["scale"])
+    if "scale" in d:
+        d["scale"] = float(d["scale"])
     return d
+
+
+def mask_args(d):
+    window = tuple(int(x) for x in d["window"]) if "window" in d else (-1, -1)
+    return dict(causal=bool(d["causal"]), window=window, alibi=d.get("alibi"))
 
 
 def test_fixture_set_is_complete():
     assert {"c1", "select_bf16", "select_f16"} <= set(FIXTURES)
     assert len(FIXTURES) >= 7
+    assert len(MASK) >= 3 and len(FP8) >= 2 and len(APPEND) >= 2
+
+
+@pytest.mark.parametrize("name", MASK)
+def test_oracle_reproduces_mask_fixture(name):
+    d = load(name)
+    got = po.attn_f64(d["q"], d["k"], d["v"], d["block_table"], d["seqlens"], d["scale"], d["dtype_code"],
+                      **mask_args(d))
+    assert np.max(np.abs(got - d["expected"])) < 1e-9
+
+
+@pytest.mark.parametrize("name", FP8)
+def test_oracle_reproduces_fp8_fixture(name):
+    d = load(name)
+    got = po.attn8_f64(d["q"], d["k8"], d["v8"], d["block_table"], d["seqlens"], d["scale"], d["dtype_code"],
+                       k_scale=d["k_scale"], v_scale=d["v_scale"], causal=bool(d["causal"]))
+    assert np.max(np.abs(got - d["expected"])) < 1e-9
+
+
+@pytest.mark.parametrize("name", APPEND)
+def test_oracle_reproduces_append_fixture(name):
+    d = load(name)
+    nk, nv = d["k_new"], d["v_new"]
+    if "k_scale" in d:
+        nk = po.quantize_e4m3(nk, d["dtype_code"], d["k_scale"])
+        nv = po.quantize_e4m3(nv, d["dtype_code"], d["v_scale"])
+    got_k, got_v = po.append_kv(d["k_cache"], d["v_cache"], d["block_table"], d["seqlens"], nk, nv)
+    np.testing.assert_array_equal(got_k, d["expected_k"])
+    np.testing.assert_array_equal(got_v, d["expected_v"])
+
+
+def test_fixture_quantiser_matches_the_oracle_quantiser():
+    """The fixtures' E4M3 encoder (nearest code by table search, sign kept) and the oracle's
+    arithmetic one agree on a log-uniform sweep with the edge values."""
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    import make_golden
+
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(100000) * np.exp(rng.uniform(-12, 7, 100000))
+    x = np.concatenate([x, [0.0, -0.0, 448, 464, 465, 500, -1e6, 2.0 ** -10, -2.0 ** -10, 2.0 ** -11,
+                            -2.0 ** -11, 3 * 2.0 ** -11, 2.0 ** -9 * 1.0625]]).astype(np.float32)
+    np.testing.assert_array_equal(make_golden.e4m3_encode(x), po.f32_to_e4m3(x))
 
 
 @pytest.mark.parametrize("name", FIXTURES)
@@ -73,3 +133,60 @@ def test_hip_path_matches_fixture(name, path, splits):
         assert (out == want).all()
     else:
         assert np.max(np.abs(got - d["expected"])) < TOL[d["dtype_code"]]
+
+
+def _close(out, want, dtype):
+    got = po.bits_to_f32(out, dtype)
+    excess = np.abs(got - want) - (TOL[dtype] + REL[dtype] * np.abs(want))
+    assert np.max(excess) < 0, float(np.max(np.abs(got - want)))
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+@pytest.mark.parametrize("splits", [0, 1, 3])
+@pytest.mark.parametrize("name", MASK + FP8)
+def test_hip_path_matches_mask_and_fp8_fixtures(name, splits):
+    import pagedkv
+    from test_gpu_fp8 import f32, i32, to_dev8
+    from test_gpu_parity import announce, from_dev, to_dev, torch_mod
+
+    torch = torch_mod()
+    d = load(name)
+    announce("golden", name, "splits", splits)
+    dt = d["dtype_code"]
+    if name in FP8:
+        k, v = to_dev8(d["k8"]), to_dev8(d["v8"])
+        extra = dict(causal=bool(d["causal"]), k_scale=f32(d["k_scale"]), v_scale=f32(d["v_scale"]))
+    else:
+        k, v = to_dev(d["k"], dt), to_dev(d["v"], dt)
+        m = mask_args(d)
+        extra = dict(causal=m["causal"], window_size=m["window"], alibi_slopes=f32(m["alibi"]))
+    out = pagedkv.decode(to_dev(d["q"], dt), k, v, i32(d["block_table"]), i32(d["seqlens"]), d["scale"], splits,
+                         **extra)
+    torch.cuda.synchronize()
+    _close(from_dev(out), d["expected"], dt)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+@pytest.mark.parametrize("name", APPEND)
+def test_hip_append_matches_fixture(name):
+    import pagedkv
+    from test_gpu_fp8 import f32, from_dev8, i32, to_dev8
+    from test_gpu_parity import announce, from_dev, to_dev, torch_mod
+
+    torch = torch_mod()
+    d = load(name)
+    announce("golden", name)
+    dt = d["dtype_code"]
+    fp8 = "k_scale" in d
+    kc = to_dev8(d["k_cache"]) if fp8 else to_dev(d["k_cache"], dt)
+    vc = to_dev8(d["v_cache"]) if fp8 else to_dev(d["v_cache"], dt)
+    scales = dict(k_scale=f32(d["k_scale"]), v_scale=f32(d["v_scale"])) if fp8 else {}
+    pagedkv.append_kv(to_dev(d["k_new"], dt), to_dev(d["v_new"], dt), kc, vc, i32(d["block_table"]),
+                      i32(d["seqlens"]), **scales)
+    torch.cuda.synchronize()
+    got_k = from_dev8(kc) if fp8 else from_dev(kc)
+    got_v = from_dev8(vc) if fp8 else from_dev(vc)
+    np.testing.assert_array_equal(got_k, d["expected_k"])
+    np.testing.assert_array_equal(got_v, d["expected_v"])
