@@ -165,6 +165,21 @@ int64_t streams_per_row(const Resolved& r) { return r.Hk * r.head_groups; }
 // Query rows per partial slot of the tile-balanced schedule.
 int64_t part_heads(const Resolved& r) { return std::min<int64_t>(r.rows, r.heads_per_wave); }
 
+// Gang of the tile-balanced schedule: 2^s waves of a workgroup share one unit
+// share and stream adjacent streams of it, so a CU reads 2^s adjacent head
+// rows of each token row together.  The largest 2^s <= 2^PKV_GANG_SHIFT_MAX
+// dividing both the streams per row and the workgroup's waves.
+#ifndef PKV_GANG_SHIFT_MAX
+#define PKV_GANG_SHIFT_MAX 2
+#endif
+int gang_shift(const Resolved& r) {
+    int s = PKV_GANG_SHIFT_MAX;
+    while (s > 0 && (streams_per_row(r) % (int64_t{1} << s) != 0 || pkv::kTileWaves % (1 << s) != 0)) {
+        --s;
+    }
+    return s;
+}
+
 // Waves of the tile-balanced schedule: one workgroup per CU, fewer when the
 // upper bound of the call's tiles (every row at max_seqlen, or at the span a
 // left window leaves) would leave a wave with under kMinTilesPerWorker tiles.
@@ -304,6 +319,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.num_groups = static_cast<int32_t>((items + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup);
     p.tile_workers = tiles ? plan.splits : 0;
     p.part_heads = static_cast<int32_t>(part_heads(r));
+    p.gang_shift = tiles ? gang_shift(r) : 0;
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;
     p.q_len = static_cast<int32_t>(r.M);
     p.rows = static_cast<int32_t>(r.rows);
@@ -360,6 +376,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.row_cap = p.row_cap;
         c.tile_workers = p.tile_workers;
         c.part_heads = p.part_heads;
+        c.gang_shift = p.gang_shift;
         c.batch = p.batch;
         c.group = p.group;
         c.head_groups = p.head_groups;

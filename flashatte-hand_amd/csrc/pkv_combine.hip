@@ -169,11 +169,34 @@ __device__ __forceinline__ RowUnits row_units(const CombineParams& p, int32_t b,
     return ru;
 }
 
-// Tile-balanced schedule: row (b, h) belongs to stream r = b * spr + u; the
-// workers w_a .. w_b owning its tiles are found from cache_seqlens with the
-// partition's unit arithmetic.  One worker means the partition already wrote
+// Where stream u of row b left its partials (tile-balanced schedule, gangs of
+// G = 2^gang_shift waves): the gangs g_a .. g_b owning its tiles, found from
+// cache_seqlens with the partition's unit arithmetic, and the slot of part 0;
+// part k is in slot slot0 + G k.
+struct StreamParts {
+    int32_t parts; // g_b - g_a + 1
+    int64_t slot0;
+};
+
+__device__ __forceinline__ StreamParts stream_parts(const CombineParams& p, const RowUnits& ru, int32_t b, int32_t u) {
+    const int gs = p.gang_shift;
+    const int sps = ((p.num_heads / p.group) * p.head_groups) >> gs;
+    const int us = u >> gs; // super-stream of row b
+    const int64_t first =
+        static_cast<int64_t>(sps) * ru.before + static_cast<int64_t>(us) * stream_units(ru.nb) + kHeaderTiles;
+    const TilePlan plan = make_tile_plan(static_cast<int64_t>(sps) * ru.all, p.tile_workers >> gs);
+    const int32_t ga = tile_worker_of(first, plan.total, plan.workers);
+    const int32_t gb = tile_worker_of(first + ru.nb - 1, plan.total, plan.workers);
+    StreamParts sp;
+    sp.parts = gb - ga + 1;
+    sp.slot0 = ((static_cast<int64_t>(ga) + static_cast<int64_t>(b) * sps + us) << gs) + (u & ((1 << gs) - 1));
+    return sp;
+}
+
+// Tile-balanced schedule: row (b, h) belongs to stream u of row b; its parts
+// are located by stream_parts.  One part means the partition already wrote
 // the row; a row without tokens gets zeros; otherwise the partials in slots
-// w_a + r .. w_b + r are merged with their LSEs, kBatch partial rows in flight
+// slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
 // at a time: 16, or for streams of many parts (long rows) as many as 128
 // registers hold, so such a row takes one round trip instead of several.
 template <bool BF16, int D, int kBatch>
@@ -195,7 +218,6 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     const int r = i * p.group + (h - kvh * p.group);
     const int hg = r / p.heads_per_wave;
     const int hn = r - p.heads_per_wave * hg;
-    const int spr = (p.num_heads / p.group) * p.head_groups;
     const int u = kvh * p.head_groups + hg;
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
 
@@ -208,23 +230,15 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
         }
         return;
     }
-    const int64_t before = ru.before;
-    const int64_t total = static_cast<int64_t>(spr) * ru.all;
-    // Unit of the stream's first tile.
-    const int64_t first =
-        static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
-    const TilePlan plan = make_tile_plan(total, p.tile_workers);
-    const int32_t wa = tile_worker_of(first, plan.total, plan.workers);
-    const int32_t wb = tile_worker_of(first + nb - 1, plan.total, plan.workers);
-    if (wa == wb) {
+    const StreamParts sp = stream_parts(p, ru, b, u);
+    if (sp.parts == 1) {
         return;
     }
-    const int parts = wb - wa + 1;
-    const int64_t slot0 = static_cast<int64_t>(wa) + static_cast<int64_t>(b) * spr + u;
-    const float* __restrict__ lse = p.part_lse + slot0 * p.part_heads + hn;
-    const float* __restrict__ po = p.part_o + (slot0 * p.part_heads + hn) * D + lane * E;
-    const int64_t lse_stride = p.part_heads;
-    const int64_t o_stride = static_cast<int64_t>(p.part_heads) * D;
+    const int parts = sp.parts;
+    const float* __restrict__ lse = p.part_lse + sp.slot0 * p.part_heads + hn;
+    const float* __restrict__ po = p.part_o + (sp.slot0 * p.part_heads + hn) * D + lane * E;
+    const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+    const int64_t o_stride = lse_stride * D;
 
     // One round trip for the common case: the first 64 parts' LSEs (lane k holds
     // part k) and the first kBatch partial rows are loaded together.
@@ -350,23 +364,16 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
         }
         return;
     }
-    const int64_t before = ru.before;
-    const int64_t total = static_cast<int64_t>(spr) * ru.all;
-    const int64_t first =
-        static_cast<int64_t>(spr) * before + static_cast<int64_t>(u) * stream_units(nb) + kHeaderTiles;
-    const TilePlan plan = make_tile_plan(total, p.tile_workers);
-    const int32_t wa = tile_worker_of(first, plan.total, plan.workers);
-    const int32_t wb = tile_worker_of(first + nb - 1, plan.total, plan.workers);
-    if (wa == wb) {
+    const StreamParts sp = stream_parts(p, ru, b, u);
+    if (sp.parts == 1) {
         return; // one worker: the partition wrote these rows
     }
-    const int parts = wb - wa + 1;
-    const int64_t slot0 = static_cast<int64_t>(wa) + static_cast<int64_t>(b) * spr + u;
-    // Row r's part k: LSE at (slot0 + k) * part_heads + r_first + r, O row likewise.
-    const float* __restrict__ lse = p.part_lse + slot0 * p.part_heads + r_first;
-    const float* __restrict__ po = p.part_o + (slot0 * p.part_heads + r_first) * D + lane * E;
-    const int64_t ls = p.part_heads;
-    const int64_t os = static_cast<int64_t>(p.part_heads) * D;
+    const int parts = sp.parts;
+    // Row r's part k: LSE at (slot0 + G k) * part_heads + r_first + r, O row likewise.
+    const float* __restrict__ lse = p.part_lse + sp.slot0 * p.part_heads + r_first;
+    const float* __restrict__ po = p.part_o + (sp.slot0 * p.part_heads + r_first) * D + lane * E;
+    const int64_t ls = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+    const int64_t os = ls * D;
 
     // One round trip: every row's first 64 LSEs (lane k: part k) and first KB partial rows.
     float l0[RB];

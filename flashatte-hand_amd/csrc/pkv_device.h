@@ -39,6 +39,7 @@ struct PartitionParams {
     int32_t num_groups;   // workgroups in the grid
     int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
     int32_t part_heads;   // rows per partial slot in the tile-balanced schedule
+    int32_t gang_shift;   // tile-balanced schedule: 2^gang_shift waves of a workgroup share a unit share
     float scale_log2;     // softmax_scale * log2(e)
     // Query rows: each KV head serves rows = q_len * group query rows,
     // r = i * group + g for query token i and head g of the group.  With
@@ -71,6 +72,7 @@ struct CombineParams {
     // splits are then unused.
     int32_t tile_workers;
     int32_t part_heads;
+    int32_t gang_shift;   // as in PartitionParams
     int32_t batch;
     int32_t group;        // H / Hk
     int32_t head_groups;  // streams per (b, kv head)
@@ -373,6 +375,17 @@ __device__ __forceinline__ Item decode_item(int32_t item, const PartitionParams&
 // w_a(r) .. w_b(r), and w_a(r + 1) >= w_b(r).  The combine finds them with
 // w(x) = floor(((x + 1) W - 1) / T), the worker owning unit x; tile t of
 // stream r is unit spr * C_b + u * units_b + kHeaderTiles + t.
+//
+// Gangs: with gang_shift = s > 0 a worker is a gang of G = 2^s waves of one
+// workgroup and the sequence is laid over super-streams, the G consecutive
+// streams u = G q + j (j < G) of a row: sps = spr / G per row, T = sps *
+// sum_b units_b, and gang g of W (the launch's waves / G) takes units
+// [lo(g), lo(g + 1)) as above.  Member j of gang g streams the tiles of stream
+// G q + j for each super-stream q of that share, so the G waves of a CU read
+// the same tokens of adjacent KV heads: G head rows next to each other in each
+// token row.  A partial of super-stream q' = b * sps + q goes to slot
+// G (g + q') + j; the parts of stream r = G q' + j are G slots apart.  s = 0 is
+// the schedule above.
 
 // Tiles a row's streams cover: from the tile of the first key any query of the
 // row can see to the row's last tile.  Without a left window that is every

@@ -1067,12 +1067,15 @@ void partition_item_group_kernel(PartitionParams p) {
     }
 }
 
-// Tile-balanced schedule (streams, units, shares and slots as defined with
-// row_tiles and make_tile_plan in pkv_device.h): wave w streams its share,
-// segment by segment.  A segment that is a whole stream is written to the
-// output; any other leaves a partial in slot w + r for the combine.  The workgroup's LDS request is padded on the
-// host so that one workgroup occupies a CU: the dispatcher then spreads the
-// grid over all CUs instead of doubling some up while others idle.
+// Tile-balanced schedule (streams, units, shares, gangs and slots as defined
+// with row_tiles and make_tile_plan in pkv_device.h): member j of gang g
+// streams stream G q + j of each super-stream q in the gang's share, segment
+// by segment.  A segment that is a whole stream is written to the output; any
+// other leaves a partial in slot G (g + q') + j for the combine (q' the
+// super-stream's index in the call).  The members run unsynchronised.  The
+// workgroup's LDS request is padded on the host so that one workgroup occupies
+// a CU: the dispatcher then spreads the grid over all CUs instead of doubling
+// some up while others idle.
 template <typename Math, int D, bool WIDE, int DEPTH, int WAVES, bool FP8>
 __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[WAVES][2 * VTile<D>::kElems];
@@ -1083,34 +1086,39 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
     if (w >= p.tile_workers) {
         return;
     }
-    const int32_t spr = p.num_heads_k * p.head_groups;
+    const int32_t gs = p.gang_shift;
+    const int32_t g = w >> gs;              // gang
+    const int32_t j = w & ((1 << gs) - 1);  // member: stream G q + j of super-stream q
+    const int32_t sps = (p.num_heads_k * p.head_groups) >> gs;
     const RowScan scan = scan_rows(p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left, lane);
-    const TilePlan plan = make_tile_plan(static_cast<int64_t>(spr) * uniform(scan.rows_total), p.tile_workers);
-    if (w >= plan.workers) {
+    const TilePlan plan =
+        make_tile_plan(static_cast<int64_t>(sps) * uniform(scan.rows_total), p.tile_workers >> gs);
+    if (g >= plan.workers) {
         return;
     }
     uint16_t* lds = lds_tiles[wave];
 
-    // Streams the tiles among this worker's units [x0, x_end), stream by
-    // stream; partials go to slot w + r.
+    // Streams the tiles among this gang's units [x0, x_end), super-stream by
+    // super-stream; partials go to slot G (g + q') + j.
     auto run_share = [&](int64_t x0, int64_t x_end) {
         const RowTiles rt = locate_unit_row(scan, p.seqlens, p.batch, p.row_cap, p.q_len, p.win_left,
-                                            muldiv(x0, 1, spr), lane);
+                                            muldiv(x0, 1, sps), lane);
         int b = uniform(rt.b);
         int seqlen = uniform(rt.seqlen);
         int nb = uniform(rt.n);
         int first = tile_span(seqlen, p.q_len, p.win_left).first;
         int units = stream_units(nb);
-        const int64_t row_first = static_cast<int64_t>(spr) * uniform(rt.before); // first unit of row b
-        int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));
-        int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of stream (b, u)
+        const int64_t row_first = static_cast<int64_t>(sps) * uniform(rt.before); // first unit of row b
+        int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));  // super-stream of row b
+        int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of super-stream (b, u)
         while (true) {
-            // The share's tiles of stream (b, u): units [x0, x_end) minus the header.
+            // The share's tiles of super-stream (b, u): units [x0, x_end) minus the header.
             const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
             const int t_hi = static_cast<int>(min(static_cast<int64_t>(nb), x_end - vs - kHeaderTiles));
             if (t_lo < t_hi) {
-                const int kvh = u / p.head_groups;
-                const int hg = u - kvh * p.head_groups;
+                const int stream = (u << gs) + j; // this member's stream of row b
+                const int kvh = stream / p.head_groups;
+                const int hg = stream - kvh * p.head_groups;
                 const int r_first = hg * Math::kHeads;
                 const int heads_here = min(Math::kHeads, p.rows - r_first);
                 const int64_t bh_first = Math::out_row(p, b, kvh, r_first);
@@ -1131,7 +1139,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 if (t_lo == 0 && t_hi == nb) {
                     Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
                 } else {
-                    const int64_t slot = static_cast<int64_t>(w) + static_cast<int64_t>(b) * spr + u;
+                    const int64_t slot =
+                        ((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j;
                     Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane, ks.out);
                 }
             }
@@ -1139,8 +1148,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
             if (vs >= x_end) {
                 break;
             }
-            // Next stream, past rows without tokens (they own no units).
-            if (++u == spr) {
+            // Next super-stream, past rows without tokens (they own no units).
+            if (++u == sps) {
                 u = 0;
                 do {
                     ++b;
@@ -1154,7 +1163,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         }
     };
 
-    run_share(share_start(w, plan), share_start(w + 1, plan));
+    run_share(share_start(g, plan), share_start(g + 1, plan));
 }
 
 // Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
