@@ -104,9 +104,11 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
         return PKV_EINVAL;
     }
     const int64_t M = std::max<int64_t>(1, d->seqlen_q);
-    // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.
-    if (d->batch * d->num_heads * M > (int64_t{1} << 30) || d->num_pages > INT32_MAX ||
-        d->block_table_stride > INT32_MAX) {
+    // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.  Each
+    // factor is bounded before the product, so no size overflows the check itself.
+    constexpr int64_t kMaxRows = int64_t{1} << 30;
+    if (d->batch > kMaxRows || d->num_heads > kMaxRows || M > kMaxRows || d->batch * d->num_heads > kMaxRows ||
+        d->batch * d->num_heads * M > kMaxRows || d->num_pages > INT32_MAX || d->block_table_stride > INT32_MAX) {
         return PKV_EUNSUPPORTED;
     }
     r.B = d->batch;

@@ -57,6 +57,9 @@ def test_status_strings():
     ("path", 9, pagedkv.PKV_EINVAL),
     ("split_tokens", 17, pagedkv.PKV_EINVAL),        # not a multiple of 16
     ("split_tokens", -16, pagedkv.PKV_EINVAL),
+    ("batch", 1 << 40, pagedkv.PKV_EUNSUPPORTED),    # sizes whose product would overflow int64
+    ("seqlen_q", 1 << 62, pagedkv.PKV_EUNSUPPORTED),
+    ("num_pages", 1 << 31, pagedkv.PKV_EUNSUPPORTED),
 ])
 def test_invalid_descriptors_are_rejected_before_any_launch(field, value, status):
     lib = _lib.load()
