@@ -185,15 +185,50 @@ int gang_shift(const Resolved& r) {
 // Waves of the tile-balanced schedule: one workgroup per CU, fewer when the
 // upper bound of the call's tiles (every row at max_seqlen, or at the span a
 // left window leaves) would leave a wave with under kMinTilesPerWorker tiles.
-int tile_workers(const Resolved& r, int64_t max_seqlen) {
+int64_t row_tiles_bound(const Resolved& r, int64_t max_seqlen) {
     int64_t span = max_seqlen;
     if (r.win_left >= 0) {
         span = std::min<int64_t>(span, r.M + r.win_left + 16);
     }
-    const int64_t tiles = r.B * streams_per_row(r) * ((span + 15) / 16);
+    return (span + 15) / 16;
+}
+
+int tile_workers(const Resolved& r, int64_t max_seqlen) {
+    const int64_t tiles = r.B * streams_per_row(r) * row_tiles_bound(r, max_seqlen);
     const int64_t per_group = kMinTilesPerWorker * pkv::kTileWaves;
     const int64_t groups = std::clamp<int64_t>((tiles + per_group - 1) / per_group, 1, kComputeUnits);
     return static_cast<int>(groups * pkv::kTileWaves);
+}
+
+// The combine launch a single pass saves, in latency-bound tile periods (≈ 1.2 µs each).
+constexpr int64_t kCombineTiles = 3;
+
+// num_splits = 0: the single pass (one wave per (b, kv head, head group) item,
+// or a workgroup of 4 waves per item when there are fewer items than CUs, and
+// no combine) when its longest chain of tiles per wave is no longer than the
+// tile schedule's share per wave plus the combine.  Small calls take it: with
+// rows of a few tiles the tile schedule hands each wave several one- or
+// two-tile segments, each starting with dependent loads.  Measured on MI355X
+// over the evaluator's contest shapes (page size 16, bf16, 32 heads): single /
+// tile schedule 5.0-6.5 / 12.9-26.3 µs for the five with rows of <= 141 tokens,
+// 21.9 / 13.8 µs at 32 rows of <= 362 tokens on 8 KV heads, tiles ahead by
+// 3-15x beyond.
+// Only calls too small to fill the chip with the tile schedule qualify: both
+// sides are upper bounds from max_seqlen, and with ragged rows (C4's log-normal
+// lengths) the tile schedule balances the actual work while the single pass
+// waits for the longest row (C4: 749 against 231 µs).  The single pass walks a
+// row from its first token (a left window only masks), the tile schedule from
+// the window's first tile.
+bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
+    if (workers >= kComputeUnits * pkv::kTileWaves) {
+        return false;
+    }
+    const int64_t row_tiles = (max_seqlen + 15) / 16;
+    const int64_t items = r.B * streams_per_row(r);
+    const int64_t single =
+        items < kComputeUnits ? (row_tiles + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup : row_tiles;
+    const int64_t share = items * (row_tiles_bound(r, max_seqlen) + pkv::kHeaderTiles) / std::max(workers, 1);
+    return single <= share + kCombineTiles;
 }
 
 SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
@@ -203,7 +238,11 @@ SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_sp
     const int64_t max_seqlen = effective_max_seqlen(d, r);
     if (num_splits == 0) {
         if (d->split_tokens == 0) {
-            return {PKV_SCHED_TILES, tile_workers(r, max_seqlen), 0};
+            const int workers = tile_workers(r, max_seqlen);
+            if (single_pass_wins(r, max_seqlen, workers)) {
+                return {PKV_SCHED_SINGLE, 1, 0};
+            }
+            return {PKV_SCHED_TILES, workers, 0};
         }
         int64_t tok = d->split_tokens;
         int64_t s = (max_seqlen + tok - 1) / tok;

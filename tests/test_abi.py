@@ -132,10 +132,17 @@ def test_tile_schedule_plan():
     assert pagedkv.split_tokens_for(d, 0) == 0
     # one workgroup per CU once there are >= 8 tiles per wave
     assert pagedkv.num_splits_for(d, 0) == COMPUTE_UNITS * TILE_WAVES
-    # small calls: fewer workgroups, at least 8 tiles per wave (upper bound from max_seqlen)
+    # smaller calls: fewer workgroups, at least 8 tiles per wave (upper bound from max_seqlen)
+    mid = base_desc(batch=4, num_heads=8, num_heads_k=2, max_seqlen=2048, block_table_stride=32)
+    tiles = 4 * 2 * 1 * (2048 // 16)                         # B * Hk * head groups * tiles per row
+    assert pagedkv.schedule_for(mid, 0) == pagedkv.PKV_SCHED_TILES
+    assert pagedkv.num_splits_for(mid, 0) == -(-tiles // (8 * TILE_WAVES)) * TILE_WAVES
+    # small calls (rows of a few tiles) take the single pass: no combine, and no wave walks
+    # several one-tile segments
     small = base_desc(batch=1, num_heads=8, num_heads_k=2, max_seqlen=256, block_table_stride=4)
-    tiles = 1 * 2 * 1 * (256 // 16)                          # B * Hk * head groups * tiles per row
-    assert pagedkv.num_splits_for(small, 0) == -(-tiles // (8 * TILE_WAVES)) * TILE_WAVES
+    assert pagedkv.schedule_for(small, 0) == pagedkv.PKV_SCHED_SINGLE
+    assert pagedkv.num_splits_for(small, 0) == 1
+    assert pagedkv.workspace_size(small, 0) == 0
     # workspace: (workers + streams) slots of min(heads per wave, group) heads, fp32 rows + LSEs;
     # an MFMA wave takes 16 heads, or 32 when the group is larger than 16
     align = lambda x: (x + 255) // 256 * 256  # noqa: E731
@@ -155,6 +162,42 @@ def test_tile_schedule_plan():
     streams = 32 * 8 * 2
     rows = (workers + streams) * 4
     assert pagedkv.workspace_size(v, 0) == align(rows * 128 * 4) + align(rows * 4)
+
+
+# The evaluator's contest shapes (B, longest row, KV heads; 32 query heads, head_dim 128, page size
+# 16, bf16; scripts/evaluate_flashattn_submission.py:359-389) and the schedule the num_splits = 0
+# heuristic takes for each, as the reference's run_kernel passes them (max_seqlen = seqlen_k, a
+# block-table row of ceil(S / 16) pages).  Measured on MI355X, single pass / tile schedule µs:
+# 5.4 / 24.9, 5.3 / 24.9, 5.3 / 18.2, 5.0 / 26.3, 6.5 / 12.9 for the first five; then
+# 21.9 / 13.8, 109.5 / 31.1, 47.7 / 22.1, 215.1 / 50.1, 83.8 / 17.3, 134.3 / 43.3, 353.1 / 94.0,
+# 601.6 / 51.6, 625.5 / 39.5.
+CONTEST = [(4, 1, 8), (4, 2, 8), (16, 17, 4), (64, 8, 4), (16, 141, 4), (32, 362, 8), (64, 2048, 4),
+           (16, 4096, 4), (32, 4096, 8), (1, 8192, 4), (16, 12251, 4), (8, 32768, 8), (1, 58966, 8),
+           (1, 61519, 4)]
+
+
+@pytest.mark.parametrize("case", range(len(CONTEST)))
+def test_heuristic_takes_the_faster_schedule_on_the_contest_shapes(case):
+    B, S, Hk = CONTEST[case]
+    d = base_desc(batch=B, num_heads=32, num_heads_k=Hk, page_size=16, num_pages=B * -(-S // 16),
+                  block_table_stride=-(-S // 16), max_seqlen=S)
+    want = pagedkv.PKV_SCHED_SINGLE if case < 5 else pagedkv.PKV_SCHED_TILES
+    assert pagedkv.schedule_for(d, 0) == want
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
+def test_heuristic_keeps_the_tile_schedule_on_the_benchmark_configs(name):
+    """Calls that fill the chip stay on the tile schedule whatever their bounds say: C4's
+    log-normal rows made the single pass 3.2x slower when it was chosen on bounds alone."""
+    from pagedkv.configs import make_config
+
+    cfg = make_config(name)
+    d = base_desc(batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k, head_dim=cfg.head_dim,
+                  page_size=cfg.page_size, num_pages=int(cfg.block_table.max()) + 1,
+                  block_table_stride=cfg.block_table.shape[1], max_seqlen=int(cfg.seqlens.max()),
+                  dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16)
+    assert pagedkv.schedule_for(d, 0) == pagedkv.PKV_SCHED_TILES
+    assert pagedkv.num_splits_for(d, 0) == COMPUTE_UNITS * TILE_WAVES
 
 
 def test_auto_path_is_a_kernel_family():
