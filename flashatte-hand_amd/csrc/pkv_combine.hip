@@ -19,6 +19,9 @@ namespace pkv {
 // Waves (rows) per workgroup; 2, 8 and 16 measured the same.
 constexpr int kCombineWaves = 4;
 
+// Waves per output row of combine_row_group_kernel.
+constexpr int kRowGroupWaves = 8;
+
 __device__ __forceinline__ bool split_nonempty(const CombineParams& p, int seqlen, int s) {
     const TokenRange r = split_tokens_of(seqlen, p.page_shift, s, p.splits, p.split_tokens);
     return r.begin < r.end;
@@ -193,56 +196,23 @@ __device__ __forceinline__ StreamParts stream_parts(const CombineParams& p, cons
     return sp;
 }
 
-// Tile-balanced schedule: row (b, h) belongs to stream u of row b; its parts
-// are located by stream_parts.  One part means the partition already wrote
-// the row; a row without tokens gets zeros; otherwise the partials in slots
-// slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
-// at a time: 16, or for streams of many parts (long rows) as many as 128
-// registers hold, so such a row takes one round trip instead of several.
-template <bool BF16, int D, int kBatch>
-__global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
-    constexpr int E = D / 64;
+// Parts [k0, k1) of one query row (lse / po at part 0, parts lse_stride LSEs
+// and o_stride floats apart): their wave-uniform LSE max (-inf when there are
+// none or all are empty), the sum of their weights exp2(lse - max) and the
+// weighted sum of their rows (the lane's E dims).  A part whose rows saw no
+// visible key (masks) has lse = -inf and weighs 0.  One round trip for up to
+// 64 parts and kBatch rows: the LSEs (lane k holds part k0 + k) and the first
+// kBatch partial rows are loaded together; more parts take kBatch rows per
+// further round trip.
+template <int E, int kBatch>
+__device__ __forceinline__ void merge_parts(const float* __restrict__ lse, const float* __restrict__ po,
+                                            int64_t lse_stride, int64_t o_stride, int k0, int k1, int lane,
+                                            float& mx_out, float& den_out, float (&acc)[E]) {
     static_assert(kBatch <= 64 && 64 % kBatch == 0, "a batch of parts takes its weights from one LSE lane each");
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= p.rows) {
-        return;
-    }
-    // Output row (b, i, h) of [B, M, H] is query row r = i * group + g of
-    // stream (b, kv head, r / heads_per_wave).
-    const int per_b = p.q_len * p.num_heads;
-    const int b = row / per_b;
-    const int i = (row - b * per_b) / p.num_heads;
-    const int h = row - b * per_b - i * p.num_heads;
-    const int kvh = h / p.group;
-    const int r = i * p.group + (h - kvh * p.group);
-    const int hg = r / p.heads_per_wave;
-    const int hn = r - p.heads_per_wave * hg;
-    const int u = kvh * p.head_groups + hg;
-    uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
-
-    const RowUnits ru = row_units(p, b, lane);
-    const int nb = ru.nb;
-    if (nb == 0) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            dst[e] = 0;
-        }
-        return;
-    }
-    const StreamParts sp = stream_parts(p, ru, b, u);
-    if (sp.parts == 1) {
-        return;
-    }
-    const int parts = sp.parts;
-    const float* __restrict__ lse = p.part_lse + sp.slot0 * p.part_heads + hn;
-    const float* __restrict__ po = p.part_o + (sp.slot0 * p.part_heads + hn) * D + lane * E;
-    const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
-    const int64_t o_stride = lse_stride * D;
-
-    // One round trip for the common case: the first 64 parts' LSEs (lane k holds
-    // part k) and the first kBatch partial rows are loaded together.
-    const float l0 = lane < parts ? lse[lane * lse_stride] : kNegInf;
+    const int n = k1 - k0;
+    lse += k0 * lse_stride;
+    po += k0 * o_stride;
+    const float l0 = lane < n ? lse[lane * lse_stride] : kNegInf;
     float x[kBatch][E];
 #pragma unroll
     for (int v = 0; v < kBatch; ++v) {
@@ -250,23 +220,20 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
         for (int e = 0; e < E; ++e) {
             x[v][e] = 0.f;
         }
-        if (v < parts) {
+        if (v < n) {
             load_partial<E>(po + v * o_stride, x[v]);
         }
     }
     float mx = l0;
-    for (int k = lane + 64; k < parts; k += 64) {
+    for (int k = lane + 64; k < n; k += 64) {
         mx = fmaxf(mx, lse[k * lse_stride]);
     }
     mx = group_max<64>(mx);
-    float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         acc[e] = 0.f;
     }
-    // Weight of part lane; a part whose rows saw no visible key (masks) has
-    // lse = -inf and weighs 0, also when every part is empty (mx = -inf).
-    float wl = (lane < parts && l0 != kNegInf) ? fast_exp2(l0 - mx) : 0.f;
+    float wl = (lane < n && l0 != kNegInf) ? fast_exp2(l0 - mx) : 0.f;
     float den = wl;
 #pragma unroll
     for (int v = 0; v < kBatch; ++v) {
@@ -276,12 +243,11 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
             acc[e] = fmaf(wv, x[v][e], acc[e]); // x = 0 past the last part
         }
     }
-    // Long rows: the remaining parts, kBatch loads in flight at a time.
 #pragma unroll 1
-    for (int k = kBatch; k < parts; k += kBatch) {
+    for (int k = kBatch; k < n; k += kBatch) {
         if ((k & 63) == 0) {
             const int kl = k + lane;
-            const float lk = kl < parts ? lse[kl * lse_stride] : kNegInf;
+            const float lk = kl < n ? lse[kl * lse_stride] : kNegInf;
             wl = lk != kNegInf ? fast_exp2(lk - mx) : 0.f;
             den += wl;
         }
@@ -292,7 +258,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
             for (int e = 0; e < E; ++e) {
                 y[v][e] = 0.f;
             }
-            if (k + v < parts) {
+            if (k + v < n) {
                 load_partial<E>(po + (k + v) * o_stride, y[v]);
             }
         }
@@ -305,11 +271,158 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
             }
         }
     }
-    den = group_sum<64>(den);
+    mx_out = mx;
+    den_out = group_sum<64>(den);
+}
+
+// Output row `row` of [B, M, H] in the tile-balanced schedule: query row
+// r = i * group + g of stream u = kv head * head_groups + r / heads_per_wave of
+// row b, and its index hn among the stream's rows.
+struct TileRow {
+    int b;
+    int u;
+    int hn;
+};
+
+__device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
+    const int per_b = p.q_len * p.num_heads;
+    const int b = row / per_b;
+    const int i = (row - b * per_b) / p.num_heads;
+    const int h = row - b * per_b - i * p.num_heads;
+    const int kvh = h / p.group;
+    const int r = i * p.group + (h - kvh * p.group);
+    const int hg = r / p.heads_per_wave;
+    TileRow t;
+    t.b = b;
+    t.u = kvh * p.head_groups + hg;
+    t.hn = r - p.heads_per_wave * hg;
+    return t;
+}
+
+// Tile-balanced schedule: row (b, h) belongs to stream u of row b; its parts
+// are located by stream_parts.  One part means the partition already wrote
+// the row; a row without tokens gets zeros; otherwise the partials in slots
+// slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
+// at a time: 16, or for streams of many parts (long rows) as many as 128
+// registers hold, so such a row takes one round trip instead of several.
+template <bool BF16, int D, int kBatch>
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
+    constexpr int E = D / 64;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= p.rows) {
+        return;
+    }
+    const TileRow t = tile_row(p, row);
+    uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
+
+    const RowUnits ru = row_units(p, t.b, lane);
+    if (ru.nb == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            dst[e] = 0;
+        }
+        return;
+    }
+    const StreamParts sp = stream_parts(p, ru, t.b, t.u);
+    if (sp.parts == 1) {
+        return;
+    }
+    const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+    float mx;
+    float den;
+    float acc[E];
+    merge_parts<E, kBatch>(p.part_lse + sp.slot0 * p.part_heads + t.hn,
+                           p.part_o + (sp.slot0 * p.part_heads + t.hn) * D + lane * E, lse_stride, lse_stride * D, 0,
+                           sp.parts, lane, mx, den, acc);
     const float inv = den > 0.f ? 1.f / den : 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+}
+
+// Streams of very many parts (a few long rows split over the whole chip: one
+// row of 60K tokens has 256 parts per stream): a workgroup of kRowGroupWaves
+// waves per output row, wave w merging a contiguous 1/kRowGroupWaves of the
+// parts, then wave 0 merging the waves' (max, weight sum, weighted rows)
+// through LDS.  Every part's loads are then in flight in the first round trip
+// instead of one batch per round trip on one wave.  Exits before the barrier
+// depend on the row only, so they are uniform over the workgroup.
+template <bool BF16, int D, int kBatch>
+__global__ __launch_bounds__(64 * kRowGroupWaves) void combine_row_group_kernel(CombineParams p) {
+    constexpr int E = D / 64;
+    __shared__ float s_acc[kRowGroupWaves][D];
+    __shared__ float s_mx[kRowGroupWaves];
+    __shared__ float s_den[kRowGroupWaves];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row = blockIdx.x;
+    const TileRow t = tile_row(p, row);
+    uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
+
+    const RowUnits ru = row_units(p, t.b, lane);
+    if (ru.nb == 0) {
+        if (wave == 0) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                dst[e] = 0;
+            }
+        }
+        return;
+    }
+    const StreamParts sp = stream_parts(p, ru, t.b, t.u);
+    if (sp.parts == 1) {
+        return;
+    }
+    const int per = (sp.parts + kRowGroupWaves - 1) / kRowGroupWaves;
+    const int k0 = min(sp.parts, wave * per);
+    const int k1 = min(sp.parts, k0 + per);
+    const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+    float mx;
+    float den;
+    float acc[E];
+    merge_parts<E, kBatch>(p.part_lse + sp.slot0 * p.part_heads + t.hn,
+                           p.part_o + (sp.slot0 * p.part_heads + t.hn) * D + lane * E, lse_stride, lse_stride * D, k0,
+                           k1, lane, mx, den, acc);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        s_acc[wave][lane * E + e] = acc[e];
+    }
+    if (lane == 0) {
+        s_mx[wave] = mx;
+        s_den[wave] = den;
+    }
+    __syncthreads();
+    if (wave != 0) {
+        return;
+    }
+    float m = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kRowGroupWaves; ++w) {
+        m = fmaxf(m, s_mx[w]);
+    }
+    float tot = 0.f;
+    float out[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        out[e] = 0.f;
+    }
+    // A wave whose parts are all empty (or that has none) has mx = -inf and
+    // weighs 0; so does every wave when all parts are empty (m = -inf).
+#pragma unroll
+    for (int w = 0; w < kRowGroupWaves; ++w) {
+        const float sc = s_mx[w] == kNegInf ? 0.f : fast_exp2(s_mx[w] - m);
+        tot = fmaf(sc, s_den[w], tot);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            out[e] = fmaf(sc, s_acc[w][lane * E + e], out[e]);
+        }
+    }
+    const float inv = tot > 0.f ? 1.f / tot : 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        dst[e] = from_f32<BF16>(out[e] * inv);
     }
 }
 
@@ -480,6 +593,10 @@ static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, c
         const int spr = (p.num_heads / p.group) * p.head_groups;
         const int waves = p.batch * spr * ((p.part_heads + kStreamRows - 1) / kStreamRows);
         launch_kernel(combine_streams_kernel<BF16, D>, dim3((waves + kWaves - 1) / kWaves), dim3(64 * kWaves), 0,
+                      stream, ev, p);
+    } else if (p.tile_workers > 0 && p.row_groups) {
+        constexpr int kGroupBatch = 64 / (D / 64) < 32 ? 64 / (D / 64) : 32;
+        launch_kernel(combine_row_group_kernel<BF16, D, kGroupBatch>, dim3(p.rows), dim3(64 * kRowGroupWaves), 0,
                       stream, ev, p);
     } else if (p.tile_workers > 0 && p.long_rows) {
         constexpr int kLong = 128 / (D / 64) < 64 ? 128 / (D / 64) : 64;

@@ -81,6 +81,7 @@ struct CombineParams {
     int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
     int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
     int32_t long_rows;    // tile schedule, a row per wave: many parts per stream, all in one round trip
+    int32_t row_groups;   // tile schedule, a workgroup per row: very many parts per stream (few long rows)
 };
 
 // Query rows per wave of the tile schedule's stream combine.
