@@ -204,8 +204,8 @@ int tile_workers(const Resolved& r, int64_t max_seqlen) {
 constexpr int64_t kCombineTiles = 3;
 
 // num_splits = 0: the single pass (one wave per (b, kv head, head group) item,
-// or a workgroup of 4 waves per item when there are fewer items than CUs, and
-// no combine) when its longest chain of tiles per wave is no longer than the
+// or a workgroup of 4 waves per item when there are no more items than CUs,
+// and no combine) when its longest chain of tiles per wave is no longer than the
 // tile schedule's share per wave plus the combine.  Small calls take it: with
 // rows of a few tiles the tile schedule hands each wave several one- or
 // two-tile segments, each starting with dependent loads.  Measured on MI355X
@@ -226,7 +226,7 @@ bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
     const int64_t row_tiles = (max_seqlen + 15) / 16;
     const int64_t items = r.B * streams_per_row(r);
     const int64_t single =
-        items < kComputeUnits ? (row_tiles + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup : row_tiles;
+        items <= kComputeUnits ? (row_tiles + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup : row_tiles;
     const int64_t share = items * (row_tiles_bound(r, max_seqlen) + pkv::kHeaderTiles) / std::max(workers, 1);
     return single <= share + kCombineTiles;
 }

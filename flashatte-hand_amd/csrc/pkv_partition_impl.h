@@ -992,7 +992,7 @@ void partition_split_kernel(PartitionParams p) {
     }
 }
 
-// Split schedules with fewer items than CUs (small batches): one workgroup per
+// Split schedules with no more items than CUs (small batches): one workgroup per
 // item, its waves taking consecutive quarters of the item's tiles; each wave
 // then parks its finished accumulator in its own LDS tile and wave 0 merges
 // the four (online-softmax merge) and writes the item's output or partial.
@@ -1202,8 +1202,8 @@ static void launch_tiles(const PartitionParams& p, hipStream_t stream, const Lau
 template <typename Math, int D, bool WIDE, bool FP8>
 static void launch_split(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     const dim3 block(64 * kWavesPerGroup);
-    if (p.num_items < kComputeUnits) {
-        // Fewer items than CUs: a workgroup per item, latency-bound, two tiles in flight.
+    if (p.num_items <= kComputeUnits) {
+        // No more items than CUs: a workgroup per item, latency-bound, two tiles in flight.
         launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems, FP8>, dim3(p.num_items), block,
                       0, stream, ev, p);
     } else {
