@@ -23,7 +23,7 @@ constexpr int kCombineWaves = 4;
 constexpr int kRowGroupWaves = 8;
 
 __device__ __forceinline__ bool split_nonempty(const CombineParams& p, int seqlen, int s) {
-    const TokenRange r = split_tokens_of(seqlen, p.page_shift, s, p.splits, p.split_tokens);
+    const TokenRange r = visible_split_tokens(seqlen, p.q_len, p.win_left, p.page_shift, s, p.splits, p.split_tokens);
     return r.begin < r.end;
 }
 

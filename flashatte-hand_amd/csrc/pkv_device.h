@@ -295,27 +295,13 @@ __device__ __forceinline__ float xor_lane(float x) {
 // streams the same amount and ragged rows simply own fewer items.
 // split_tokens == 0: split s covers pages [n*s/S, n*(s+1)/S) of the row's n
 // valid pages (best_flashattn_kvcache_decode.cu:664-671), so any two splits of
-// a row differ by at most one page.  Either way the range may be empty.
+// a row differ by at most one page.  Either way the range may be empty, and a
+// left window clips it to the keys some query can see (visible_split_tokens,
+// after tile_span).
 struct TokenRange {
     int32_t begin;
     int32_t end;
 };
-
-__device__ __forceinline__ TokenRange split_tokens_of(int32_t seqlen, int32_t page_shift, int32_t split,
-                                                      int32_t splits, int32_t split_tokens) {
-    TokenRange r;
-    if (split_tokens > 0) {
-        r.begin = split * split_tokens;
-        r.end = max(r.begin, min(r.begin + split_tokens, seqlen));
-        return r;
-    }
-    const int32_t pages = seqlen > 0 ? ((seqlen - 1) >> page_shift) + 1 : 0;
-    const int32_t first = static_cast<int32_t>((static_cast<int64_t>(pages) * split) / splits);
-    const int32_t last = static_cast<int32_t>((static_cast<int64_t>(pages) * (split + 1)) / splits);
-    r.begin = first << page_shift;
-    r.end = first < last ? min(last << page_shift, seqlen) : r.begin;
-    return r;
-}
 
 // Work items of the split schedules: item = (split * B + b) * units + u with
 // u = kv head * head_groups + head group, so consecutive waves (and
@@ -399,9 +385,37 @@ struct TileSpan {
 
 __device__ __forceinline__ TileSpan tile_span(int32_t sl, int32_t q_len, int32_t win_left) {
     TileSpan t;
-    t.first = win_left >= 0 ? (min(max(sl - q_len - win_left, 0), sl) >> 4) : 0;
+    // 64-bit: a window near INT32_MAX (practically unbounded) must not wrap.
+    const int64_t lo = static_cast<int64_t>(sl) - q_len - win_left;
+    t.first = win_left >= 0 ? static_cast<int32_t>(min(max(lo, int64_t{0}), static_cast<int64_t>(sl)) >> 4) : 0;
     t.n = ((sl + 15) >> 4) - t.first;
     return t;
+}
+
+// Tokens of split `split` of a row of seqlen tokens (split schedules), within
+// the span some query can see: a left window masks everything before the
+// tile of its first key for every query, so no split reads it.  Page-balanced
+// splits divide the pages of that span as the reference divides a row's pages
+// (best:664-671; the whole row without a window); token windows are clipped
+// to it.  With one split the range is the span itself, non-empty for any row
+// with tokens.  The partition and the combine both take ranges from here.
+__device__ __forceinline__ TokenRange visible_split_tokens(int32_t seqlen, int32_t q_len, int32_t win_left,
+                                                           int32_t page_shift, int32_t split, int32_t splits,
+                                                           int32_t split_tokens) {
+    const int32_t lo = tile_span(seqlen, q_len, win_left).first * 16;
+    TokenRange r;
+    if (split_tokens > 0) {
+        r.begin = max(split * split_tokens, lo);
+        r.end = max(r.begin, min(split * split_tokens + split_tokens, seqlen));
+        return r;
+    }
+    const int32_t p0 = lo >> page_shift;
+    const int32_t pages = seqlen > 0 ? ((seqlen - 1) >> page_shift) + 1 - p0 : 0;
+    const int32_t first = p0 + static_cast<int32_t>((static_cast<int64_t>(pages) * split) / splits);
+    const int32_t last = p0 + static_cast<int32_t>((static_cast<int64_t>(pages) * (split + 1)) / splits);
+    r.begin = max(first << page_shift, lo);
+    r.end = first < last ? min(last << page_shift, seqlen) : r.begin;
+    return r;
 }
 
 __device__ __forceinline__ int32_t clamped_seqlen(const int32_t* __restrict__ seqlens, int32_t b, int32_t row_cap) {

@@ -959,7 +959,8 @@ void partition_split_kernel(PartitionParams p) {
 
     const int seqlen = min(p.seqlens[b], p.row_cap);
     Math::set_mask(p, b, seqlen, heads_here, lane, q);
-    const TokenRange range = split_tokens_of(seqlen, p.page_shift, split, p.splits, p.split_tokens);
+    const TokenRange range =
+        visible_split_tokens(seqlen, p.q_len, p.win_left, p.page_shift, split, p.splits, p.split_tokens);
 
     if (range.begin >= range.end) {
         // Empty range.  With one split the row has no tokens: its output is 0.
@@ -1019,7 +1020,8 @@ void partition_item_group_kernel(PartitionParams p) {
     Math::load_q(p, it.b, it.kvh, r_first, heads_here, lane, q);
     const int seqlen = min(p.seqlens[it.b], p.row_cap);
     Math::set_mask(p, it.b, seqlen, heads_here, lane, q);
-    const TokenRange range = split_tokens_of(seqlen, p.page_shift, it.split, p.splits, p.split_tokens);
+    const TokenRange range =
+        visible_split_tokens(seqlen, p.q_len, p.win_left, p.page_shift, it.split, p.splits, p.split_tokens);
     if (range.begin >= range.end) {
         // As in partition_split_kernel: zeros for an empty row, nothing for an empty split.
         if (p.splits == 1 && wave == 0) {

@@ -66,3 +66,27 @@ def test_long_rows_match_oracle(case):
     else:
         want = po.attn_f64(q, kc, vc, bt, lens, scale, dtype, causal=causal)
     assert_close(out, want, dtype)
+
+
+@pytest.mark.parametrize("splits", [1, 3, 0])
+@pytest.mark.parametrize("window", [(64, 0), (2**31 - 2, -1)])
+def test_left_windows_over_long_rows_for_every_schedule(splits, window):
+    """A left window bounds what every schedule reads: split ranges (the single pass and forced
+    page-balanced splits) start at the tile of the earliest visible key, like the tile schedule's
+    streams, and a window near INT32_MAX (practically unbounded) clips nothing."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("long-rows-window", splits, window)
+    rng = np.random.default_rng(5300 + splits)
+    lens = np.array([20000, 1, 9000, 70], dtype=np.int32)
+    B, H, Hk, D, P, M, dtype = len(lens), 16, 4, 128, 32, 4, 1
+    _, kc, vc, bt, _ = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=lens, dtype=dtype)
+    q = rand_bits(rng, (B, M, H, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    out = pagedkv.decode(to_dev(q, dtype), to_dev(kc, dtype), to_dev(vc, dtype), i32(bt), i32(lens), scale, splits,
+                         causal=True, window_size=window)
+    torch.cuda.synchronize()
+    oracle_window = window if window[0] < 2**30 else (-1, -1)
+    want = po.attn_f64(q, kc, vc, bt, lens, scale, dtype, causal=True, window=oracle_window)
+    assert_close(out, want, dtype)
