@@ -213,21 +213,24 @@ constexpr int64_t kCombineTiles = 3;
 // tile schedule 5.0-6.5 / 12.9-26.3 µs for the five with rows of <= 141 tokens,
 // 21.9 / 13.8 µs at 32 rows of <= 362 tokens on 8 KV heads, tiles ahead by
 // 3-15x beyond.
-// Only calls too small to fill the chip with the tile schedule qualify: both
-// sides are upper bounds from max_seqlen, and with ragged rows (C4's log-normal
-// lengths) the tile schedule balances the actual work while the single pass
-// waits for the longest row (C4: 749 against 231 µs).  The single pass walks a
-// row from its first token (a left window only masks), the tile schedule from
-// the window's first tile.
+// Both sides are upper bounds from max_seqlen (both schedules start a row at
+// a left window's first tile).  Without a window that bounds every row, only
+// calls too small to fill the chip with the tile schedule qualify: with ragged
+// rows (C4's log-normal lengths) the tile schedule balances the actual work
+// while the single pass waits for the longest row (C4: 749 against 231 µs).
+// A window bounds every row's span to about M + window tokens, so the spans
+// of rows longer than the window are equal and the bound is tight (C2 with a
+// 1024-token window: single pass 25.5 µs, tile schedule 28.7).
 bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
-    if (workers >= kComputeUnits * pkv::kTileWaves) {
+    const bool window_bounds_rows = r.win_left >= 0 && r.M + r.win_left + 16 < max_seqlen;
+    if (!window_bounds_rows && workers >= kComputeUnits * pkv::kTileWaves) {
         return false;
     }
-    const int64_t row_tiles = (max_seqlen + 15) / 16;
+    const int64_t span_tiles = row_tiles_bound(r, max_seqlen);
     const int64_t items = r.B * streams_per_row(r);
     const int64_t single =
-        items <= kComputeUnits ? (row_tiles + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup : row_tiles;
-    const int64_t share = items * (row_tiles_bound(r, max_seqlen) + pkv::kHeaderTiles) / std::max(workers, 1);
+        items <= kComputeUnits ? (span_tiles + pkv::kWavesPerGroup - 1) / pkv::kWavesPerGroup : span_tiles;
+    const int64_t share = items * (span_tiles + pkv::kHeaderTiles) / std::max(workers, 1);
     return single <= share + kCombineTiles;
 }
 

@@ -361,10 +361,18 @@ def test_workspace_counts_query_rows():
 
 
 def test_left_window_shrinks_the_tile_schedule():
-    """A left window bounds every row's span to about M + window tokens, so small
-    windows get fewer waves (each still with at least 8 tiles)."""
-    full = pagedkv.num_splits_for(base_desc(max_seqlen=65536), 0)
-    small = pagedkv.num_splits_for(base_desc(max_seqlen=65536, window_size=(64, 0)), 0)
-    assert full == 1024
-    # 32 rows x 8 KV heads x ceil((1 + 64 + 16) / 16) = 6 tiles = 1536 tiles: 48 workgroups of 4 waves.
-    assert small == 192
+    """A left window bounds every row's span to about M + window tokens: the tile schedule gets
+    fewer waves (each still with at least 8 tiles), and when the window bounds every row the
+    spans are equal, so the single pass (no combine) takes calls whose chains it keeps short."""
+    assert pagedkv.num_splits_for(base_desc(max_seqlen=65536), 0) == 1024
+    # 2 rows x 8 KV heads x ceil((1 + 2048 + 16) / 16) = 130 tiles = 2080 tiles: 65 workgroups of 4 waves.
+    mid = base_desc(batch=2, max_seqlen=65536, window_size=(2048, 0))
+    assert pagedkv.schedule_for(mid, 0) == pagedkv.PKV_SCHED_TILES
+    assert pagedkv.num_splits_for(mid, 0) == 260
+    # 32 rows x 8 KV heads with a 64-token window: chains of 2 tiles per wave in the single pass.
+    small = base_desc(max_seqlen=65536, window_size=(64, 0))
+    assert pagedkv.schedule_for(small, 0) == pagedkv.PKV_SCHED_SINGLE
+    assert pagedkv.workspace_size(small, 0) == 0
+    # C2 with a 1024-token window: 25.5 µs single pass against 28.7 µs tile schedule on MI355X.
+    c2w = base_desc(max_seqlen=4096, window_size=(1024, -1))
+    assert pagedkv.schedule_for(c2w, 0) == pagedkv.PKV_SCHED_SINGLE
