@@ -76,8 +76,8 @@ typedef struct pkv_decode_desc {
     int32_t dtype;              /* PKV_DTYPE_F16 or PKV_DTYPE_BF16 (q, caches and out share it) */
     int32_t path;               /* PKV_PATH_* */
     int32_t split_tokens;       /* num_splits == 0 only: tokens per split window (multiple of 16);
-                                   0 = the tile-balanced schedule (or, for small calls,
-                                   the single pass) */
+                                   0 = the tile-balanced schedule (or, for small or
+                                   windowed calls, the single pass) */
     int32_t reserved;           /* must be 0 */
     void* workspace;            /* device memory for split partials; may be NULL when splits == 1 */
     size_t workspace_bytes;
@@ -121,9 +121,10 @@ typedef struct pkv_decode_desc {
  *       which read cache_seqlens on the device, so every wave streams the same
  *       bytes however ragged the rows are, and a combine merges the rows that
  *       more than one wave touched.  Calls too small to fill the chip
- *       (rows of a few tiles, judged from max_seqlen) take the single pass
- *       instead when its longest chain of tiles per wave is no longer: no
- *       combine, and no wave walks several short segments.  With
+ *       (rows of a few tiles, judged from max_seqlen), and calls whose left
+ *       window bounds every row, take the single pass instead when its
+ *       longest chain of tiles per wave is no longer: no combine, and no
+ *       wave walks several short segments.  With
  *       desc->split_tokens > 0, fixed windows of that many tokens;
  *   1 = single pass writing `out` directly;
  *   n > 1 = forced: each row's valid pages are divided into n near-equal
