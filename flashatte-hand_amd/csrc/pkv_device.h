@@ -37,6 +37,8 @@ struct PartitionParams {
     int32_t batch;        // B
     int32_t num_items;    // splits * B * Hk * head_groups
     int32_t num_groups;   // workgroups in the grid
+    int32_t item_groups;  // split schedules: a workgroup of waves per item (no more items than CUs,
+                          // items of two tiles or more)
     int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
     int32_t part_heads;   // rows per partial slot in the tile-balanced schedule
     int32_t gang_shift;   // tile-balanced schedule: 2^gang_shift waves of a workgroup share a unit share

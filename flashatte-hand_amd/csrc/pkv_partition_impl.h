@@ -1204,7 +1204,7 @@ static void launch_tiles(const PartitionParams& p, hipStream_t stream, const Lau
 template <typename Math, int D, bool WIDE, bool FP8>
 static void launch_split(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
     const dim3 block(64 * kWavesPerGroup);
-    if (p.num_items <= kComputeUnits) {
+    if (p.item_groups) {
         // No more items than CUs: a workgroup per item, latency-bound, two tiles in flight.
         launch_kernel(partition_item_group_kernel<Math, D, WIDE, kSplitDepthFewItems, FP8>, dim3(p.num_items), block,
                       0, stream, ev, p);
