@@ -26,7 +26,7 @@ from test_gpu_parity import announce, from_dev, to_dev, torch_mod
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
 
-CASES = 96
+CASES = 200
 MAX_WORK = 2e9  # B * M * H * longest row * D: keeps the fp64 oracle within about a second
 
 
