@@ -1,0 +1,57 @@
+"""The reference evaluator's contest shapes through the C++ harness.
+
+The 14 (batch, longest row, KV heads) cases of scripts/evaluate_flashattn_submission.py:359-389
+(32 query heads, head_dim 128, page size 16, bf16, num_splits = 0, row lengths from the
+evaluator's formula), each run by `pkv_harness --case ... --profile contest --entry run_kernel
+--check`: the reference-compatible entry, the harness's own checks, event timing.  Prints the
+harness's JSON line per case, then a markdown table; exits 1 if any case fails its checks.
+
+    python flashatte-hand_amd/harness/contest.py [--harness PATH] [--entry run_kernel|pkv_decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+CONTEST = [(4, 1, 8), (4, 2, 8), (16, 17, 4), (64, 8, 4), (16, 141, 4), (32, 362, 8), (64, 2048, 4),
+           (16, 4096, 4), (32, 4096, 8), (1, 8192, 4), (16, 12251, 4), (8, 32768, 8), (1, 58966, 8),
+           (1, 61519, 4)]
+SCHEDULES = {1: "single", 2: "pages", 3: "windows", 4: "tiles"}
+HARNESS = Path(__file__).resolve().parents[1] / "lib" / "pkv_harness"
+
+
+def run_case(harness: Path, batch: int, seqlen: int, kv_heads: int, entry: str) -> dict:
+    cmd = [str(harness), "--case", f"{batch},{seqlen},1,32,{kv_heads},128,16", "--profile", "contest",
+           "--entry", entry, "--check"]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+    if res.returncode not in (0, 1):
+        raise RuntimeError(f"{' '.join(cmd)} exited with {res.returncode}: {res.stderr.strip()}")
+    return json.loads(res.stdout.strip().splitlines()[-1])
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--harness", type=Path, default=HARNESS)
+    ap.add_argument("--entry", choices=("run_kernel", "pkv_decode"), default="run_kernel")
+    args = ap.parse_args(argv)
+    if not args.harness.exists():
+        print(f"{args.harness} is not built (pagedkv.build.build_harness())", file=sys.stderr)
+        return 2
+    rows, ok = [], True
+    for batch, seqlen, kv_heads in CONTEST:
+        d = run_case(args.harness, batch, seqlen, kv_heads, args.entry)
+        print(json.dumps(d), flush=True)
+        ok = ok and bool(d["check"]["ok"])
+        c = d["case"]
+        rows.append(f"| {batch} | {seqlen} | {kv_heads} | {c['seqlen_sum']:,} | {SCHEDULES.get(d['schedule'], d['schedule'])}"
+                    f" | {d['us_per_call']:.1f} | {d['kv_gbps']:,.0f} | {'ok' if d['check']['ok'] else 'FAILED'} |")
+    print("\n| B | longest row | Hk | tokens | schedule | µs/call | KV GB/s | checks |\n|--:|--:|--:|--:|---|--:|--:|---|")
+    print("\n".join(rows))
+    return 0 if ok else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

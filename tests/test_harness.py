@@ -75,3 +75,19 @@ def test_harness_checks_pass(args):
     if "--entry" in args or ("--case" in args and "--dtype" not in args):
         assert check["entries_identical"] is True
     assert line["us_per_call"] > 0
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+def test_contest_runner_passes_every_case():
+    """harness/contest.py: the reference evaluator's 14 contest shapes through run_kernel, every
+    case passing the harness's checks, one table row each."""
+    import sys
+
+    runner = PKG_DIR / "harness" / "contest.py"
+    res = subprocess.run([sys.executable, str(runner)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                         timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
+    lines = [json.loads(x) for x in res.stdout.splitlines() if x.startswith("{")]
+    assert len(lines) == 14 and all(d["check"]["ok"] for d in lines)
+    assert res.stdout.count("| ok |") == 14
