@@ -22,10 +22,20 @@ namespace {
 // gfx950 (MI355X) compute units; the tile-balanced schedule sizes its grid against it.
 constexpr int kComputeUnits = pkv::kComputeUnits;
 
-// Tile-balanced schedule: one workgroup of pkv::kTileWaves waves per CU, and
-// no fewer than this many 16-token tiles per wave (each wave's share starts
-// with a few dependent loads that more tiles amortise).
-constexpr int64_t kMinTilesPerWorker = 8;
+// Tile-balanced schedule: one workgroup of pkv::kTileWaves waves per CU.  A
+// call fills the chip when it has kFillTilesPerWorker 16-token tiles per wave
+// for every wave; smaller calls get no fewer than PKV_MIN_TILES_PER_WORKER
+// tiles per wave (each wave's share starts with a few dependent loads that
+// more tiles amortise, but on a chip the call does not fill, fewer tiles per
+// wave shorten the chain).  Measured on MI355X, 8 -> 2 tiles: the evaluator's
+// default shapes with 8 heads of 256 dims, 1-4 rows of 512-2048 tokens
+// 15.4-22.5 -> 12.7-20.7 µs, its 8192-token single row 16.6 -> 14.3 µs; calls
+// that fill the chip (C2-C5) unchanged.
+constexpr int64_t kFillTilesPerWorker = 8;
+#ifndef PKV_MIN_TILES_PER_WORKER
+#define PKV_MIN_TILES_PER_WORKER 2
+#endif
+constexpr int64_t kMinTilesPerWorker = PKV_MIN_TILES_PER_WORKER;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
@@ -193,9 +203,9 @@ int64_t row_tiles_bound(const Resolved& r, int64_t max_seqlen) {
     return (span + 15) / 16;
 }
 
-int tile_workers(const Resolved& r, int64_t max_seqlen) {
+int tile_workers(const Resolved& r, int64_t max_seqlen, int64_t min_tiles = kMinTilesPerWorker) {
     const int64_t tiles = r.B * streams_per_row(r) * row_tiles_bound(r, max_seqlen);
-    const int64_t per_group = kMinTilesPerWorker * pkv::kTileWaves;
+    const int64_t per_group = min_tiles * pkv::kTileWaves;
     const int64_t groups = std::clamp<int64_t>((tiles + per_group - 1) / per_group, 1, kComputeUnits);
     return static_cast<int>(groups * pkv::kTileWaves);
 }
@@ -223,7 +233,8 @@ constexpr int64_t kCombineTiles = 3;
 // 1024-token window: single pass 25.5 µs, tile schedule 28.7).
 bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
     const bool window_bounds_rows = r.win_left >= 0 && r.M + r.win_left + 16 < max_seqlen;
-    if (!window_bounds_rows && workers >= kComputeUnits * pkv::kTileWaves) {
+    const bool fills_chip = tile_workers(r, max_seqlen, kFillTilesPerWorker) >= kComputeUnits * pkv::kTileWaves;
+    if (!window_bounds_rows && fills_chip) {
         return false;
     }
     const int64_t span_tiles = row_tiles_bound(r, max_seqlen);

@@ -1,12 +1,16 @@
-"""The reference evaluator's contest shapes through the C++ harness.
+"""The reference evaluator's shape sets through the C++ harness.
 
-The 14 (batch, longest row, KV heads) cases of scripts/evaluate_flashattn_submission.py:359-389
-(32 query heads, head_dim 128, page size 16, bf16, num_splits = 0, row lengths from the
-evaluator's formula), each run by `pkv_harness --case ... --profile contest --entry run_kernel
---check`: the reference-compatible entry, the harness's own checks, event timing.  Prints the
-harness's JSON line per case, then a markdown table; exits 1 if any case fails its checks.
+`--set contest` (default): the 14 (batch, longest row, KV heads) cases of
+scripts/evaluate_flashattn_submission.py:359-389 (32 query heads, head_dim 128, page size 16,
+bf16, row lengths from the evaluator's formula).  `--set legacy-smoke`: its default set's smoke
+subset (eval:339-357: batch 1-8, every row at 512 / 2048 / 8192 tokens, 8 query and 8 KV heads,
+head_dim 256, page size 16).  Each case runs as `pkv_harness --case ... --profile contest|legacy
+--entry run_kernel --check`: the reference-compatible entry, the harness's own checks, event
+timing.  Prints the harness's JSON line per case, then a markdown table; exits 1 if any case
+fails its checks.
 
-    python flashatte-hand_amd/harness/contest.py [--harness PATH] [--entry run_kernel|pkv_decode]
+    python flashatte-hand_amd/harness/contest.py [--set contest|legacy-smoke] [--harness PATH]
+                                                 [--entry run_kernel|pkv_decode]
 """
 from __future__ import annotations
 
@@ -19,12 +23,15 @@ from pathlib import Path
 CONTEST = [(4, 1, 8), (4, 2, 8), (16, 17, 4), (64, 8, 4), (16, 141, 4), (32, 362, 8), (64, 2048, 4),
            (16, 4096, 4), (32, 4096, 8), (1, 8192, 4), (16, 12251, 4), (8, 32768, 8), (1, 58966, 8),
            (1, 61519, 4)]
+# (batch, seqlen, query heads, KV heads, head_dim): eval:339-357 with smoke = True.
+LEGACY_SMOKE = [(b, s, 8, 8, 256) for s in (512, 2048, 8192) for b in (1, 2, 4, 8)]
 SCHEDULES = {1: "single", 2: "pages", 3: "windows", 4: "tiles"}
 HARNESS = Path(__file__).resolve().parents[1] / "lib" / "pkv_harness"
 
 
-def run_case(harness: Path, batch: int, seqlen: int, kv_heads: int, entry: str) -> dict:
-    cmd = [str(harness), "--case", f"{batch},{seqlen},1,32,{kv_heads},128,16", "--profile", "contest",
+def run_case(harness: Path, batch: int, seqlen: int, heads: int, kv_heads: int, head_dim: int, profile: str,
+             entry: str) -> dict:
+    cmd = [str(harness), "--case", f"{batch},{seqlen},1,{heads},{kv_heads},{head_dim},16", "--profile", profile,
            "--entry", entry, "--check"]
     res = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
     if res.returncode not in (0, 1):
@@ -36,13 +43,18 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--harness", type=Path, default=HARNESS)
     ap.add_argument("--entry", choices=("run_kernel", "pkv_decode"), default="run_kernel")
+    ap.add_argument("--set", choices=("contest", "legacy-smoke"), default="contest")
     args = ap.parse_args(argv)
     if not args.harness.exists():
         print(f"{args.harness} is not built (pagedkv.build.build_harness())", file=sys.stderr)
         return 2
     rows, ok = [], True
-    for batch, seqlen, kv_heads in CONTEST:
-        d = run_case(args.harness, batch, seqlen, kv_heads, args.entry)
+    if args.set == "contest":
+        cases = [(b, s, 32, k, 128, "contest") for b, s, k in CONTEST]
+    else:
+        cases = [(b, s, h, k, d, "legacy") for b, s, h, k, d in LEGACY_SMOKE]
+    for batch, seqlen, heads, kv_heads, head_dim, profile in cases:
+        d = run_case(args.harness, batch, seqlen, heads, kv_heads, head_dim, profile, args.entry)
         print(json.dumps(d), flush=True)
         ok = ok and bool(d["check"]["ok"])
         c = d["case"]

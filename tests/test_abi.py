@@ -132,11 +132,11 @@ def test_tile_schedule_plan():
     assert pagedkv.split_tokens_for(d, 0) == 0
     # one workgroup per CU once there are >= 8 tiles per wave
     assert pagedkv.num_splits_for(d, 0) == COMPUTE_UNITS * TILE_WAVES
-    # smaller calls: fewer workgroups, at least 8 tiles per wave (upper bound from max_seqlen)
+    # smaller calls: fewer workgroups, at least 2 tiles per wave (upper bound from max_seqlen)
     mid = base_desc(batch=4, num_heads=8, num_heads_k=2, max_seqlen=2048, block_table_stride=32)
     tiles = 4 * 2 * 1 * (2048 // 16)                         # B * Hk * head groups * tiles per row
     assert pagedkv.schedule_for(mid, 0) == pagedkv.PKV_SCHED_TILES
-    assert pagedkv.num_splits_for(mid, 0) == -(-tiles // (8 * TILE_WAVES)) * TILE_WAVES
+    assert pagedkv.num_splits_for(mid, 0) == -(-tiles // (2 * TILE_WAVES)) * TILE_WAVES
     # small calls (rows of a few tiles) take the single pass: no combine, and no wave walks
     # several one-tile segments
     small = base_desc(batch=1, num_heads=8, num_heads_k=2, max_seqlen=256, block_table_stride=4)
@@ -370,14 +370,15 @@ def test_workspace_counts_query_rows():
 
 
 def test_left_window_shrinks_the_tile_schedule():
-    """A left window bounds every row's span to about M + window tokens: the tile schedule gets
-    fewer waves (each still with at least 8 tiles), and when the window bounds every row the
-    spans are equal, so the single pass (no combine) takes calls whose chains it keeps short."""
+    """A left window bounds every row's span to about M + window tokens: the tile schedule sizes
+    its grid for that span, and when the window bounds every row the spans are equal, so the
+    single pass (no combine) takes calls whose chains it keeps short."""
     assert pagedkv.num_splits_for(base_desc(max_seqlen=65536), 0) == 1024
-    # 2 rows x 8 KV heads x ceil((1 + 2048 + 16) / 16) = 130 tiles = 2080 tiles: 65 workgroups of 4 waves.
-    mid = base_desc(batch=2, max_seqlen=65536, window_size=(2048, 0))
+    # 1 row x 2 KV heads x ceil((1 + 2048 + 16) / 16) = 130 tiles = 260 tiles: 33 workgroups of 4 waves
+    # (at least 2 tiles each; the call does not fill the chip).
+    mid = base_desc(batch=1, num_heads=8, num_heads_k=2, max_seqlen=65536, window_size=(2048, 0))
     assert pagedkv.schedule_for(mid, 0) == pagedkv.PKV_SCHED_TILES
-    assert pagedkv.num_splits_for(mid, 0) == 260
+    assert pagedkv.num_splits_for(mid, 0) == 132
     # 32 rows x 8 KV heads with a 64-token window: chains of 2 tiles per wave in the single pass.
     small = base_desc(max_seqlen=65536, window_size=(64, 0))
     assert pagedkv.schedule_for(small, 0) == pagedkv.PKV_SCHED_SINGLE

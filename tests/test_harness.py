@@ -79,15 +79,16 @@ def test_harness_checks_pass(args):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
-def test_contest_runner_passes_every_case():
-    """harness/contest.py: the reference evaluator's 14 contest shapes through run_kernel, every
-    case passing the harness's checks, one table row each."""
+@pytest.mark.parametrize("which, n", [("contest", 14), ("legacy-smoke", 12)])
+def test_shape_set_runner_passes_every_case(which, n):
+    """harness/contest.py: the reference evaluator's contest shapes and its default set's smoke
+    subset through run_kernel, every case passing the harness's checks, one table row each."""
     import sys
 
     runner = PKG_DIR / "harness" / "contest.py"
-    res = subprocess.run([sys.executable, str(runner)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
-                         timeout=300)
+    res = subprocess.run([sys.executable, str(runner), "--set", which], stdout=subprocess.PIPE,
+                         stderr=subprocess.PIPE, text=True, timeout=300)
     assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
     lines = [json.loads(x) for x in res.stdout.splitlines() if x.startswith("{")]
-    assert len(lines) == 14 and all(d["check"]["ok"] for d in lines)
-    assert res.stdout.count("| ok |") == 14
+    assert len(lines) == n and all(d["check"]["ok"] for d in lines)
+    assert res.stdout.count("| ok |") == n
