@@ -121,6 +121,14 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
         d->batch * d->num_heads * M > kMaxRows || d->num_pages > INT32_MAX || d->block_table_stride > INT32_MAX) {
         return PKV_EUNSUPPORTED;
     }
+    // The partition kernels address the 16 token rows of a tile with 32-bit
+    // byte offsets from the tile's page base (token stride Hk * D elements):
+    // 16 rows must span less than 4 GiB.  (Hk <= H <= 2^30 and D <= 256, so the
+    // product fits in 64 bits.)
+    const int64_t kv_elem_bytes = d->kv_dtype == PKV_KV_DTYPE_FP8_E4M3 ? 1 : 2;
+    if (16 * d->num_heads_k * d->head_dim * kv_elem_bytes >= (int64_t{1} << 32)) {
+        return PKV_EUNSUPPORTED;
+    }
     r.B = d->batch;
     r.H = d->num_heads;
     r.Hk = d->num_heads_k;

@@ -68,9 +68,12 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(CombinePara
     const int64_t sr = (static_cast<int64_t>(b) * (p.num_heads / p.group) + kvh) * p.q_len * p.group +
                        i * p.group + (h - kvh * p.group);
     const int seqlen = min(p.seqlens[b], p.row_cap);
-    // Splits past the last token window are empty in split_tokens mode.
+    // Splits past the last token window are empty in split_tokens mode (the
+    // last split runs to the row's end, so a row longer than splits windows
+    // has all of them).
     const int n_loop = p.split_tokens > 0
-                           ? (seqlen > 0 ? min(p.splits, (seqlen + p.split_tokens - 1) / p.split_tokens) : 0)
+                           ? (seqlen > 0 ? min(p.splits, seqlen / p.split_tokens + (seqlen % p.split_tokens != 0))
+                                         : 0)
                            : p.splits;
     const float* __restrict__ lse = p.part_lse + sr * p.splits;
     const float* __restrict__ o = p.part_o + sr * p.splits * D + lane * E;

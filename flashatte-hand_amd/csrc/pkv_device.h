@@ -227,6 +227,12 @@ __device__ __forceinline__ float dpp_f32(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+// Value of the lane 8 above within each row of 16 lanes (DPP row_shl:8); 0 in
+// lanes 8-15, whose source lies outside the row.
+__device__ __forceinline__ float lanes_up8(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x108, 0xf, 0xf, true));
+}
+
 // ds_swizzle in bit mode: lane i reads lane (i & and) | or) ^ xor within each 32-lane half.
 template <int XOR_MASK>
 __device__ __forceinline__ float swizzle_xor_f32(float x) {
@@ -407,8 +413,12 @@ __device__ __forceinline__ TokenRange visible_split_tokens(int32_t seqlen, int32
     const int32_t lo = tile_span(seqlen, q_len, win_left).first * 16;
     TokenRange r;
     if (split_tokens > 0) {
+        // The window count comes from the host's max_seqlen; the last window
+        // runs to the row's end, so a row longer than that bound is still
+        // read whole.  (split * split_tokens < max_seqlen: no overflow.)
         r.begin = max(split * split_tokens, lo);
-        r.end = max(r.begin, min(split * split_tokens + split_tokens, seqlen));
+        const int32_t stop = split + 1 == splits ? seqlen : min(split * split_tokens + split_tokens, seqlen);
+        r.end = max(r.begin, stop);
         return r;
     }
     const int32_t p0 = lo >> page_shift;

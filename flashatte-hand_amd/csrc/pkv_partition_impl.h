@@ -17,10 +17,11 @@
 //     MfmaMath  16 or 32 query rows per wave (zero-padded).  S^T[16 tok x 16
 //               rows] = K Q^T with v_mfma_f32_16x16x32_{bf16,f16} (A = K from
 //               LDS, lane (n, j): token n, dims 8(4kk + j) .. +7; B = Q^T in
-//               VGPRs), then O^T[D x 16 rows] += V^T P^T with
-//               v_mfma_f32_16x16x16{bf16_1k,f16}, V^T from the LDS tile through
-//               ds_read_b64_tr_b16 and P^T packed to 16 bits in place; a second
-//               block of 16 rows reuses the same K and V^T operands;
+//               VGPRs), then O^T[D x 16 rows] += V^T P^T with the same
+//               MFMA over (token, part) pairs: V^T from the LDS tile through
+//               ds_read_b64_tr_b16 (each column twice), P^T as a 16-bit head
+//               and a 16-bit remainder of the fp32 probabilities, packed in
+//               place; a second block of 16 rows reuses the K and V^T operands;
 //     ValuMath  1, 2 or 4 heads per wave.  Lane (t, c) takes token t and a
 //               quarter of the dims: v_dot2 products, a cross-row sum, DPP row
 //               max/sum; PV with fp32 FMAs, each lane owning D/64 dims of
@@ -44,13 +45,14 @@ namespace pkv {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// v_mfma_f32_16x16x32_{bf16,f16}: C[16 x 16] += A[16 x 32] B[32 x 16], lane
+// (n, j) holding A[n][8j .. 8j + 7] and B[8j .. 8j + 7][n], C[4j .. 4j + 3][n].
+// QK^T and PV both use it (PV over (token, head / remainder) pairs).
 template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_qk(const uint4& a, const uint4& b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_16x16x32(const uint4& a, const uint4& b, f32x4 c) {
     if constexpr (BF16) {
         return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                        0, 0, 0);
@@ -60,8 +62,12 @@ __device__ __forceinline__ f32x4 mfma_qk(const uint4& a, const uint4& b, f32x4 c
     }
 }
 
+// v_mfma_f32_16x16x16{bf16_1k,f16}: the same with K = 16, lane (n, j) holding
+// A[n][4j .. 4j + 3] and B[4j .. 4j + 3][n].
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_pv(const uint2& a, const uint2& b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_16x16x16(const uint2& a, const uint2& b, f32x4 c) {
     if constexpr (BF16) {
         return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
                                                          0, 0, 0);
@@ -70,6 +76,12 @@ __device__ __forceinline__ f32x4 mfma_pv(const uint2& a, const uint2& b, f32x4 c
                                                      0, 0);
     }
 }
+
+// PV form: 0 = one 16x16x32 MFMA per output tile over (token, head /
+// remainder) pairs, 1 = two 16x16x16 MFMAs (heads, then remainders).
+#ifndef PKV_PV_TWO_MFMA
+#define PKV_PV_TWO_MFMA 0
+#endif
 
 // Cache element width: 2 bytes (fp16 / bf16, the compute dtype) or 1 byte
 // (OCP FP8 e4m3, converted to the compute dtype when staged).  Either way a
@@ -255,12 +267,27 @@ __device__ __forceinline__ int64_t query_out_row(const PartitionParams& p, int b
 // NB blocks of 16 query rows per wave share each staged K/V tile: the K
 // A operand and the V^T reads are loaded once and feed NB QK and NB PV MFMA
 // chains, so a (b, kv head) with up to 16 NB query rows reads its K/V once.
-template <bool BF16, int D, bool MQ, int NB>
+//
+// The PV product carries each probability as a 16-bit head plus a 16-bit
+// remainder (see tile()).  COLS (one block of at most 8 query rows): rows 0-7
+// also occupy MFMA columns 8-15 (lane n computes row n mod 8), columns 0-7
+// take the heads and columns 8-15 the remainders through one 16x16x16 MFMA,
+// and finish() adds column n + 8 to column n.  Otherwise both parts go along
+// K through a 16x16x32 MFMA whose A operand holds each V^T column twice.
+template <bool BF16, int D, bool MQ, int NB, bool COLS = false>
 struct MfmaMath {
+    static_assert(!COLS || NB == 1, "column split: one block of at most 8 rows");
     static constexpr int kHeads = 16 * NB;
     static constexpr int DT = D / 16;
     static constexpr bool kMultiQuery = MQ;
     static constexpr bool kBF16 = BF16;
+    // Probabilities are taken as 2^(s - m + offset).  fp16 has a narrow
+    // exponent range: an offset of 7 puts p in (0, 2^15] (below fp16's 65504
+    // with the lazy threshold of 2^8) and moves the point where small p and
+    // their remainders lose bits to subnormals 7 octaves further down.  bf16
+    // has fp32's exponent range and needs none.  O and l carry the same
+    // factor, so O / l is unchanged and the LSE subtracts it.
+    static constexpr float kProbLog2Offset = BF16 ? 0.f : 7.f;
 
     // QK B operands: row 16 nb + n of the slice (n = lane & 15), dims
     // 8(4kk + j) .. +7 (zero past the slice).  MQ: per block, the lane's row
@@ -296,12 +323,16 @@ struct MfmaMath {
         }
     }
 
+    // Query row (within the block) whose scores lane computes: its MFMA column,
+    // or the column mod 8 with COLS (columns 8-15 repeat rows 0-7).
+    __device__ static int row_lane(int lane) { return COLS ? (lane & 7) : (lane & 15); }
+
     __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int rows_here, int lane,
                                   Q& q) {
         const int j = lane >> 4;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const int n = 16 * nb + (lane & 15);
+            const int n = 16 * nb + row_lane(lane);
             int64_t row;
             if constexpr (MQ) {
                 const int r = r_first + min(n, rows_here - 1);
@@ -330,7 +361,7 @@ struct MfmaMath {
             int all_hi = seqlen;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const int n = 16 * nb + (lane & 15);
+                const int n = 16 * nb + row_lane(lane);
                 const int pos = seqlen - p.q_len + q.qi[nb];
                 int lo = 0;
                 int hi = seqlen;
@@ -393,7 +424,7 @@ struct MfmaMath {
             s[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < D / 32; ++kk) {
-                s[nb] = mfma_qk<BF16>(ka[kk], q.op[nb][kk], s[nb]);
+                s[nb] = mfma_16x16x32<BF16>(ka[kk], q.op[nb][kk], s[nb]);
             }
         }
         // Lane holds row 16 nb + n, tokens 4j + i.  MQ: tiles every row sees
@@ -445,12 +476,18 @@ struct MfmaMath {
                 a.m[nb] = m_new;
             }
         }
-        uint2 pb[NB];
+        // P^T as the PV B operand: the fp32 probabilities split into a 16-bit
+        // head and a 16-bit remainder, so the MFMA sums p v with p carried to
+        // ~2x the 16-bit precision, and the denominator (the fp32 p) matches
+        // it.  Lane (n, j) holds tokens 4j .. 4j + 3 of its row: heads in
+        // elements 0-3 and remainders in 4-7 (stacked along K), or with COLS
+        // the heads in columns 0-7 and the remainders in columns 8-15.
+        uint4 pb[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             // MQ: a row that has seen no visible key yet has m = -inf and only
             // masked scores; measure them from 0 so they give exactly 0.
-            const float mref = (MQ && a.m[nb] == kNegInf) ? 0.f : a.m[nb];
+            const float mref = ((MQ && a.m[nb] == kNegInf) ? 0.f : a.m[nb]) - kProbLog2Offset;
             float pr[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -459,6 +496,13 @@ struct MfmaMath {
             a.l[nb] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
             pb[nb].x = pack2_hw<BF16>(pr[0], pr[1]);
             pb[nb].y = pack2_hw<BF16>(pr[2], pr[3]);
+            // The head is pr rounded to nearest, so pr - head is exact in fp32
+            // (Sterbenz); its own rounding leaves a relative error of u^2.
+            float h0, h1, h2, h3;
+            unpack2<BF16>(pb[nb].x, h0, h1);
+            unpack2<BF16>(pb[nb].y, h2, h3);
+            pb[nb].z = pack2_hw<BF16>(pr[0] - h0, pr[1] - h1);
+            pb[nb].w = pack2_hw<BF16>(pr[2] - h2, pr[3] - h3);
         }
 
         // O^T tile dt: A = V^T needs V[4j + i][16 dt + n] (i = 0..3) in lane (n, j).
@@ -475,20 +519,59 @@ struct MfmaMath {
                 (lds_s16x4*)((__attribute__((address_space(3))) uint16_t*)(rd + 16 * dt)));
             av[dt] = __builtin_bit_cast(uint2, t);
         }
+        if constexpr (COLS) {
+            const bool rem = (lane & 15) >= 8;
+            const uint2 b = make_uint2(rem ? pb[0].z : pb[0].x, rem ? pb[0].w : pb[0].y);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a.o[0][dt] = mfma_16x16x16<BF16>(av[dt], b, a.o[0][dt]);
+            }
+            return;
+        }
+#if PKV_PV_TWO_MFMA
+        // Two 16x16x16 MFMAs per output tile, against the heads and then the
+        // remainders (all heads first, so no MFMA waits on the one before).
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = mfma_pv<BF16>(av[dt], pb[nb], a.o[nb][dt]);
+                a.o[nb][dt] = mfma_16x16x16<BF16>(av[dt], make_uint2(pb[nb].x, pb[nb].y), a.o[nb][dt]);
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                a.o[nb][dt] = mfma_16x16x16<BF16>(av[dt], make_uint2(pb[nb].z, pb[nb].w), a.o[nb][dt]);
             }
         }
+#else
+        // 16x16x32 MFMA over (token, part) pairs: A holds each token's V^T
+        // column twice (once against the head, once against the remainder).
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint4 a2 = make_uint4(av[dt].x, av[dt].y, av[dt].x, av[dt].y);
+                a.o[nb][dt] = mfma_16x16x32<BF16>(a2, pb[nb], a.o[nb][dt]);
+            }
+        }
+#endif
     }
 
     // l holds this lane's 4-token partial sums; total over the 4 lanes of row n.
+    // COLS: column n + 8 holds the remainders' share of row n's O: add it to
+    // column n (lanes 8-15 are then unused).
     __device__ static void finish(Acc& a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             a.l[nb] = sum_halves32(sum_rows16(a.l[nb]));
+        }
+        if constexpr (COLS) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    a.o[0][dt][i] += lanes_up8(a.o[0][dt][i]);
+                }
+            }
         }
     }
 
@@ -540,7 +623,7 @@ struct MfmaMath {
                                     a.o[nb][dt][3] * inv);
                 }
                 if (j == 0) {
-                    p.part_lse[pi] = a.l[nb] > 0.f ? a.m[nb] + fast_log2(a.l[nb]) : kNegInf;
+                    p.part_lse[pi] = a.l[nb] > 0.f ? (a.m[nb] - kProbLog2Offset) + fast_log2(a.l[nb]) : kNegInf;
                 }
             }
         }
@@ -872,14 +955,22 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 }
 
 // Attention of one head slice over tokens [begin, end) (begin < end), the page
-// window already loaded at win_base = begin / P.  Leaves Math's accumulator
-// (unnormalised O, reference max, denominator) finished.
+// window already loaded at some win_base <= begin / P.  Leaves Math's
+// accumulator (unnormalised O, reference max, denominator) finished.
 template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
 __device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
                                              int win_base, const typename Math::Q& q, uint16_t* lds, int begin,
                                              int end, int lane, int kvh, typename Math::Acc& acc, float scale_log2) {
     Math::init(acc);
     const int last_page = (end - 1) >> p.page_shift;
+    // The first tile is loaded without a window check: its page must be one
+    // of the 64 the window holds.  A window loaded ahead of the range (fixed
+    // token windows load theirs at the split's start, before a left window
+    // has clipped the range's front) is moved to the range's first page.
+    if ((begin >> p.page_shift) - win_base >= 64) {
+        win_base = begin >> p.page_shift;
+        win = load_page_window(bt_row, win_base, last_page, lane, p.num_pages);
+    }
     if (last_page - win_base < 64) {
         // Common case: the whole range fits in one page window.
         tile_loop<Math, D, WIDE, DEPTH, false, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
@@ -1257,10 +1348,14 @@ static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wa
             }
             return launch_math<MfmaMath<BF16, D, false, 2>, D>(p, stream, ev);
         }
+        // At most 8 query rows per KV head: the remainders take the padding columns.
+        const bool cols = p.rows <= 8;
         if (multi_query) {
-            return launch_math<MfmaMath<BF16, D, true, 1>, D>(p, stream, ev);
+            return cols ? launch_math<MfmaMath<BF16, D, true, 1, true>, D>(p, stream, ev)
+                        : launch_math<MfmaMath<BF16, D, true, 1>, D>(p, stream, ev);
         }
-        return launch_math<MfmaMath<BF16, D, false, 1>, D>(p, stream, ev);
+        return cols ? launch_math<MfmaMath<BF16, D, false, 1, true>, D>(p, stream, ev)
+                    : launch_math<MfmaMath<BF16, D, false, 1>, D>(p, stream, ev);
     }
     if (multi_query) {
         return hipErrorInvalidValue; // the VALU policy has one query token and no mask

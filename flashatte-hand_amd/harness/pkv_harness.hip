@@ -87,39 +87,45 @@ __device__ inline float hash_normal(uint64_t seed, uint64_t i) {
 
 // n elements of N(0, sigma) as 16-bit values; with peak_prob > 0 each row of
 // `row` elements is scaled by peak_factor with that probability.
+// Grid-stride: the largest evaluator pools hold more than 2^32 elements, past
+// a dispatch's 32-bit grid size, so the grids are capped (grid_for).
 __global__ void fill_normal_kernel(uint16_t* dst, int64_t n, int row, uint64_t seed, float sigma, float peak_prob,
                                    float peak_factor, int bf16) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= n) {
-        return;
-    }
-    float x = sigma * hash_normal(seed, static_cast<uint64_t>(i));
-    if (peak_prob > 0.f) {
-        const uint64_t r = static_cast<uint64_t>(i / row);
-        const float u = static_cast<float>(mix64(~seed + r * kGolden) >> 40) * 0x1.0p-24f;
-        x = u < peak_prob ? x * peak_factor : x;
-    }
-    if (bf16) {
-        const __hip_bfloat16 h = __float2bfloat16(x);
-        dst[i] = *reinterpret_cast<const uint16_t*>(&h);
-    } else {
-        const __half h = __float2half(x);
-        dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float x = sigma * hash_normal(seed, static_cast<uint64_t>(i));
+        if (peak_prob > 0.f) {
+            const uint64_t r = static_cast<uint64_t>(i / row);
+            const float u = static_cast<float>(mix64(~seed + r * kGolden) >> 40) * 0x1.0p-24f;
+            x = u < peak_prob ? x * peak_factor : x;
+        }
+        if (bf16) {
+            const __hip_bfloat16 h = __float2bfloat16(x);
+            dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+        } else {
+            const __half h = __float2half(x);
+            dst[i] = *reinterpret_cast<const uint16_t*>(&h);
+        }
     }
 }
 
 // dst page perm[p] = src page p (pages of page_elems 16-bit elements).
 __global__ void permute_pages_kernel(const uint16_t* src, uint16_t* dst, const int32_t* perm, int64_t pages,
                                      int64_t page_elems) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= pages * page_elems) {
-        return;
+    const int64_t n = pages * page_elems;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int64_t p = i / page_elems;
+        dst[static_cast<int64_t>(perm[p]) * page_elems + (i - p * page_elems)] = src[i];
     }
-    const int64_t p = i / page_elems;
-    dst[static_cast<int64_t>(perm[p]) * page_elems + (i - p * page_elems)] = src[i];
 }
 
 int64_t blocks_for(int64_t n, int threads) { return (n + threads - 1) / threads; }
+
+// Workgroups of a grid-stride launch over n elements: at most 2^20 (2^28 threads of 256).
+unsigned grid_for(int64_t n, int threads) {
+    return static_cast<unsigned>(std::min<int64_t>(std::max<int64_t>(blocks_for(n, threads), 1), int64_t{1} << 20));
+}
 
 // ------------------------------------------------------------------ 16-bit values on the host
 
@@ -320,7 +326,7 @@ std::vector<T> from_dev(const T* src, size_t n) {
 
 void fill(uint16_t* dst, int64_t n, int row, uint64_t seed, float sigma, float peak_prob, bool bf16) {
     const int threads = 256;
-    fill_normal_kernel<<<dim3(static_cast<unsigned>(blocks_for(n, threads))), dim3(threads)>>>(
+    fill_normal_kernel<<<dim3(grid_for(n, threads)), dim3(threads)>>>(
         dst, n, row, seed, sigma, peak_prob, 8.0f, bf16 ? 1 : 0);
     hip_check(hipGetLastError(), "fill kernel");
 }
@@ -520,7 +526,7 @@ CheckResult run_checks(const Case& c, const Runner& run, const KvSet& s, uint64_
         s2.out = dev_alloc<uint16_t>(out_n);
         const int64_t page_elems = c.P * c.Hk * c.D;
         const int threads = 256;
-        const dim3 grid(static_cast<unsigned>(blocks_for(c.num_pages * page_elems, threads)));
+        const dim3 grid(grid_for(c.num_pages * page_elems, threads));
         permute_pages_kernel<<<grid, dim3(threads)>>>(s.k, s2.k, d_perm, c.num_pages, page_elems);
         permute_pages_kernel<<<grid, dim3(threads)>>>(s.v, s2.v, d_perm, c.num_pages, page_elems);
         hip_check(hipGetLastError(), "permute kernel");

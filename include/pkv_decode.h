@@ -31,7 +31,9 @@ extern "C" {
  * every entry point here reports what happened instead. */
 #define PKV_OK 0
 #define PKV_EINVAL 1           /* null pointer, non-positive or inconsistent dims, misaligned pointer */
-#define PKV_EUNSUPPORTED 2     /* dtype / head_dim / page size / path not supported for this shape */
+#define PKV_EUNSUPPORTED 2     /* dtype / head_dim / page size / path not supported for this shape, or
+                                  sizes past the kernels' index range (e.g. 16 * Hk * D * element
+                                  bytes >= 2^32: a tile's rows are addressed with 32-bit offsets) */
 #define PKV_ENOWORKSPACE 3     /* workspace missing or smaller than pkv_decode_workspace_size() */
 #define PKV_ELAUNCH 4          /* a HIP launch or runtime call failed */
 
@@ -72,7 +74,10 @@ typedef struct pkv_decode_desc {
     int64_t num_pages;          /* physical pages held by k_cache / v_cache */
     int64_t block_table_stride; /* int32 elements between consecutive block_table rows */
     int64_t max_seqlen;         /* host-known upper bound of cache_seqlens (flash-attn's seqlen_k);
-                                   0 = block_table_stride * page_size.  Used only to choose splits. */
+                                   0 = block_table_stride * page_size.  Used only to choose the
+                                   schedule and split count: a row longer than it is still read
+                                   whole (every schedule takes row lengths from cache_seqlens,
+                                   and the last fixed token window runs to the row's end). */
     int32_t dtype;              /* PKV_DTYPE_F16 or PKV_DTYPE_BF16 (q, caches and out share it) */
     int32_t path;               /* PKV_PATH_* */
     int32_t split_tokens;       /* num_splits == 0 only: tokens per split window (multiple of 16);

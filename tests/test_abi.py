@@ -72,6 +72,28 @@ def test_invalid_descriptors_are_rejected_before_any_launch(field, value, status
     assert pagedkv.num_splits_for(d, 0) == 0
 
 
+@pytest.mark.parametrize("kv_dtype,bytes_per_elem", [(pagedkv.PKV_KV_DTYPE_SAME, 2),
+                                                     (pagedkv.PKV_KV_DTYPE_FP8_E4M3, 1)])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_tile_rows_past_32_bit_offsets_are_rejected(kv_dtype, bytes_per_elem, D):
+    """The kernels address a tile's 16 token rows with 32-bit byte offsets: a
+    descriptor whose 16 * Hk * D * element bytes reaches 2^32 must be refused
+    (PKV_EUNSUPPORTED), and the largest Hk below that bound accepted."""
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    hk_limit = (1 << 32) // (16 * D * bytes_per_elem)  # smallest Hk whose tile span is 4 GiB
+    for hk, ok in ((hk_limit, False), (hk_limit - 1, True)):
+        d = base_desc(batch=1, num_heads=hk, num_heads_k=hk, head_dim=D, kv_dtype=kv_dtype)
+        assert 16 * hk * D * bytes_per_elem >= (1 << 32) or ok
+        if ok:
+            assert pagedkv.schedule_for(d, 0) != 0, (hk, D)
+        else:
+            assert pagedkv.schedule_for(d, 0) == 0, (hk, D)
+            assert pagedkv.workspace_size(d, 0) == 0
+            st = lib.pkv_decode(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None)
+            assert st == pagedkv.PKV_EUNSUPPORTED
+
+
 def test_null_and_misaligned_pointers_are_rejected():
     lib = _lib.load()
     d = base_desc()

@@ -89,10 +89,15 @@ def test_rows_without_visible_keys_in_a_segment(rng):
         assert np.max(np.abs(got - want)) < TOL[dtype], window
 
 
+@pytest.mark.parametrize("H,Hk,M", [(32, 8, 2), (32, 2, 2), (48, 2, 2)])
 @pytest.mark.parametrize("splits", [0, 1, 4])
-def test_repeated_queries_reproduce_the_single_query_bits(rng, splits):
-    announce("masked-repeat-bits", splits)
-    B, H, Hk, D, P, dtype, M = 4, 32, 8, 128, 64, 1, 4
+def test_repeated_queries_reproduce_the_single_query_bits(rng, splits, H, Hk, M):
+    """M copies of each query give the one-query bits.  The MFMA path sums each probability's
+    16-bit remainder in the padding columns when a KV head has at most 8 query rows and along K
+    otherwise, which round differently, so each case keeps both calls on one side: 4 and 8 rows,
+    16 and 32 rows (one and two 16-row blocks), 24 and 48 rows (two blocks, two head groups)."""
+    announce("masked-repeat-bits", splits, H, Hk, M)
+    B, D, P, dtype = 4, 128, 64, 1
     q1, k, v, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=[1, 64, 700, 3000], dtype=dtype)
     one = run_masked(q1, k, v, bt, sl, 0.125, dtype, splits)
     many = run_masked(np.repeat(q1, M, axis=1), k, v, bt, sl, 0.125, dtype, splits)
