@@ -312,6 +312,44 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 thread_local int t_last_status = PKV_OK;
 
+// Scratch of pkv_decode_noalloc: the split partials of one call, in a static
+// device array (each GPU the library runs on holds its own copy until the
+// process ends).  In host code `scratch` is a host-side stand-in, not a device
+// address: kernels and copies get the address that hipGetSymbolAddress
+// returns for the current device, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[PKV_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (checked against the stream's device).
+int scratch_for_stream(void* stream, void** ptr) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        return PKV_ELAUNCH;
+    }
+    if (stream != nullptr) {
+        int sdev = -1;
+        if (hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev) != hipSuccess) {
+            return PKV_ELAUNCH;
+        }
+        if (sdev != dev) {
+            return PKV_EINVAL;
+        }
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+            return PKV_ELAUNCH;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return PKV_OK;
+}
+
 // Library-owned grow-only workspace for the reference-compatible run_kernel
 // (the reference keeps the same kind of static buffer, best:17-20, 1078-1133).
 std::mutex g_legacy_mutex;
@@ -580,6 +618,33 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
                const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
                const pkv_decode_desc* desc, void* stream) {
     return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, desc, stream,
+                       true);
+}
+
+int pkv_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
+                       const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
+                       const pkv_decode_desc* desc, void* stream) {
+    if (desc == nullptr) {
+        return PKV_EINVAL;
+    }
+    // The size check is host arithmetic: an oversized plan fails before the device is touched.
+    Resolved r;
+    int st = resolve(desc, r);
+    if (st != PKV_OK) {
+        return st;
+    }
+    if (num_splits >= 0 && workspace_bytes(r, resolve_splits(desc, r, num_splits)) > PKV_SCRATCH_BYTES) {
+        return PKV_ENOWORKSPACE;
+    }
+    void* ptr = nullptr;
+    st = scratch_for_stream(stream, &ptr);
+    if (st != PKV_OK) {
+        return st;
+    }
+    pkv_decode_desc d = *desc;
+    d.workspace = ptr;
+    d.workspace_bytes = PKV_SCRATCH_BYTES;
+    return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, &d, stream,
                        true);
 }
 

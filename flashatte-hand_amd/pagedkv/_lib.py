@@ -37,10 +37,12 @@ PKV_MASK_CAUSAL = 1
 PKV_MASK_WINDOW = 2
 
 PKV_MAX_SPLITS = 256
+PKV_SCRATCH_BYTES = 32 << 20  # device scratch of pkv_decode_noalloc per GPU
 
 # Every function the header declares, with its ctypes signature.
 EXPORTS = {
     "pkv_decode": (ctypes.c_int, None),  # argtypes filled below (needs the struct)
+    "pkv_decode_noalloc": (ctypes.c_int, None),
     "pkv_decode_workspace_size": (ctypes.c_size_t, None),
     "pkv_decode_num_splits": (ctypes.c_int, None),
     "pkv_decode_split_tokens": (ctypes.c_int, None),
@@ -115,6 +117,8 @@ def load() -> ctypes.CDLL:
         ctypes.c_float, ctypes.c_int, ctypes.c_void_p,      # softmax_scale, num_splits, out
         desc_p, ctypes.c_void_p,                            # desc, stream
     ]
+    lib.pkv_decode_noalloc.restype = ctypes.c_int
+    lib.pkv_decode_noalloc.argtypes = lib.pkv_decode.argtypes
     lib.pkv_decode_workspace_size.restype = ctypes.c_size_t
     lib.pkv_decode_workspace_size.argtypes = [desc_p, ctypes.c_int]
     lib.pkv_decode_num_splits.restype = ctypes.c_int

@@ -150,6 +150,34 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache,
  * hidden grow-only workspace (best_flashattn_kvcache_decode.cu:17-20, 1078-1133). */
 size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits);
 
+/* Device scratch pkv_decode_noalloc holds on each GPU it runs on: 32 MiB. */
+#define PKV_SCRATCH_BYTES ((size_t)32 << 20)
+
+/*
+ * pkv_decode for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  No counterpart in
+ * the reference, whose run_kernel grows a hidden workspace with cudaMalloc.
+ * Same arguments and results as pkv_decode, but the split partials go to a
+ * scratch buffer of PKV_SCRATCH_BYTES in device memory that the library holds
+ * on each GPU for the life of the process (a static device array);
+ * desc->workspace and desc->workspace_bytes are ignored.  The call allocates
+ * nothing (no hipMalloc, hipFree or allocating library routine); its first
+ * call on a GPU looks up that GPU's copy of the buffer.
+ * - A plan that needs more than PKV_SCRATCH_BYTES
+ *   (pkv_decode_workspace_size(desc, num_splits) > PKV_SCRATCH_BYTES, e.g.
+ *   forced splits over very many rows) returns PKV_ENOWORKSPACE before anything
+ *   is enqueued; the heuristic plans of the benchmark configs need at most 21 MB.
+ * - `stream` must belong to the current device (PKV_EINVAL otherwise).
+ * - Every call on one GPU shares that GPU's buffer: calls that overlap on one
+ *   GPU (on other streams, from other host threads) race; serialise them.
+ * - The buffer keeps the last call's contents.  No kernel reads a partial the
+ *   same call has not written, so nothing needs clearing.
+ */
+int pkv_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                       const int32_t* block_table, const int32_t* cache_seqlens,
+                       float softmax_scale, int num_splits, void* out,
+                       const pkv_decode_desc* desc, void* stream);
+
 /* Split count pkv_decode will use for `num_splits` (0 = heuristic); for
  * PKV_SCHED_TILES, the number of partition waves sharing the tiles.
  * Replaces choose_splits (best_flashattn_kvcache_decode.cu:1039-1076, 1299-1312).
