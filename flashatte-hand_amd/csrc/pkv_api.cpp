@@ -356,12 +356,58 @@ std::mutex g_legacy_mutex;
 void* g_legacy_ws = nullptr;
 size_t g_legacy_ws_bytes = 0;
 
+// Which combine merges the tile schedule's partials.
+struct CombineForm {
+    bool by_stream;
+    bool long_rows;
+    bool row_groups;
+};
+
+CombineForm combine_form(const Resolved& r, const SplitPlan& plan) {
+    CombineForm f{};
+    if (plan.schedule != PKV_SCHED_TILES) {
+        return f;
+    }
+    // Streams split over a few workers (about workers / streams + 1 parts
+    // each, within the stream combine's first round trip) are merged four
+    // rows per wave when that still makes at least 8 waves per CU: fewer,
+    // fuller waves.  Otherwise a row per wave.  Measured: C4 8.2 -> 6.4 us
+    // and C4 with four query tokens 22 -> 13.9 us by stream; C2 (256 waves)
+    // 4.1 -> 6.6, C2 with four query tokens (1,024) 4.8 -> 7.0 and C5's
+    // five-part streams 6.6 -> 8.5 us would lose.
+    const int64_t streams = r.B * streams_per_row(r);
+    const int64_t parts_est = plan.splits / std::max<int64_t>(streams, 1) + 1;
+    const int64_t stream_waves = streams * ((part_heads(r) + pkv::kStreamRows - 1) / pkv::kStreamRows);
+    f.by_stream = stream_waves >= 8 * kComputeUnits && parts_est <= 1024 / r.D;
+    // More than 16 parts per stream (long rows, few streams: C3 has 13-52):
+    // the row-per-wave combine keeps all of them in flight at once.
+    f.long_rows = !f.by_stream && parts_est > 16;
+    // More than 64 parts per stream (a few long rows over the whole chip:
+    // one 60K-token row has 256): a workgroup of waves per row, each
+    // merging a slice of the parts.  Measured on the evaluator's single-row
+    // contest shapes (B = 1, 8K-61K tokens): the row-per-wave combine took
+    // 6.2-15.9 µs.
+    f.row_groups = !f.by_stream && parts_est > 64;
+    return f;
+}
+
+// A one-token append folded into the decode's combine (pkv_decode_append's
+// fast path): the new token's K/V rows and the caches they go into.
+struct AppendFold {
+    const void* k_new;
+    const void* v_new;
+    void* k_cache;
+    void* v_cache;
+};
+
 // pkv_decode: validation, then (when `launch`) the partition and combine
 // launches.  With launch == false only the checks run, so a caller that
-// enqueues other work first can fail before touching anything.
+// enqueues other work first can fail before touching anything.  `fold`: the
+// combine also adds and stores one appended token per row (the plan must be
+// the tile schedule with the row-per-wave combine; fold_fits checks it).
 int decode_impl(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                 const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
-                const pkv_decode_desc* desc, void* stream, bool launch) {
+                const pkv_decode_desc* desc, void* stream, bool launch, const AppendFold* fold = nullptr) {
     Resolved r;
     int st = resolve(desc, r);
     if (st != PKV_OK) {
@@ -383,6 +429,10 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     const size_t need = workspace_bytes(r, plan);
     if (need > 0 && (desc->workspace == nullptr || desc->workspace_bytes < need || !aligned16(desc->workspace))) {
         return PKV_ENOWORKSPACE;
+    }
+    if (fold != nullptr && (!tiles || r.M != 1 || r.multi_query || r.kv_fp8 ||
+                            combine_form(r, plan).by_stream || combine_form(r, plan).long_rows)) {
+        return PKV_EUNSUPPORTED;
     }
     const int64_t items = tiles ? 0 : r.B * r.Hk * r.head_groups * splits;
     if (items > INT32_MAX || (tiles && static_cast<int64_t>(plan.splits) + r.B * streams_per_row(r) > INT32_MAX)) {
@@ -429,6 +479,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.tile_workers = tiles ? plan.splits : 0;
     p.part_heads = static_cast<int32_t>(part_heads(r));
     p.gang_shift = tiles ? gang_shift(r) : 0;
+    p.force_partial = fold != nullptr ? 1 : 0;
     p.scale_log2 = softmax_scale * 1.4426950408889634074f;
     p.q_len = static_cast<int32_t>(r.M);
     p.rows = static_cast<int32_t>(r.rows);
@@ -464,26 +515,10 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.rows = static_cast<int32_t>(r.B * r.M * r.H);
         c.q_len = p.q_len;
         c.win_left = p.win_left;
-        // Streams split over a few workers (about workers / streams + 1 parts
-        // each, within the stream combine's first round trip) are merged four
-        // rows per wave when that still makes at least 8 waves per CU: fewer,
-        // fuller waves.  Otherwise a row per wave.  Measured: C4 8.2 -> 6.4 us
-        // and C4 with four query tokens 22 -> 13.9 us by stream; C2 (256 waves)
-        // 4.1 -> 6.6, C2 with four query tokens (1,024) 4.8 -> 7.0 and C5's
-        // five-part streams 6.6 -> 8.5 us would lose.
-        const int64_t streams = r.B * streams_per_row(r);
-        const int64_t parts_est = plan.splits / std::max<int64_t>(streams, 1) + 1;
-        const int64_t stream_waves = streams * ((p.part_heads + pkv::kStreamRows - 1) / pkv::kStreamRows);
-        c.by_stream = tiles && stream_waves >= 8 * kComputeUnits && parts_est <= 1024 / r.D ? 1 : 0;
-        // More than 16 parts per stream (long rows, few streams: C3 has 13-52):
-        // the row-per-wave combine keeps all of them in flight at once.
-        c.long_rows = tiles && !c.by_stream && parts_est > 16 ? 1 : 0;
-        // More than 64 parts per stream (a few long rows over the whole chip:
-        // one 60K-token row has 256): a workgroup of waves per row, each
-        // merging a slice of the parts.  Measured on the evaluator's single-row
-        // contest shapes (B = 1, 8K-61K tokens): the row-per-wave combine took
-        // 6.2-15.9 µs.
-        c.row_groups = tiles && !c.by_stream && parts_est > 64 ? 1 : 0;
+        const CombineForm form = combine_form(r, plan);
+        c.by_stream = form.by_stream ? 1 : 0;
+        c.long_rows = form.long_rows ? 1 : 0;
+        c.row_groups = form.row_groups ? 1 : 0;
         c.num_heads = static_cast<int32_t>(r.H);
         c.splits = splits;
         c.split_tokens = plan.split_tokens;
@@ -496,6 +531,17 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.group = p.group;
         c.head_groups = p.head_groups;
         c.heads_per_wave = r.heads_per_wave;
+        if (fold != nullptr) {
+            c.app_q = p.q;
+            c.app_k = static_cast<const uint16_t*>(fold->k_new);
+            c.app_v = static_cast<const uint16_t*>(fold->v_new);
+            c.app_k_cache = static_cast<uint16_t*>(fold->k_cache);
+            c.app_v_cache = static_cast<uint16_t*>(fold->v_cache);
+            c.app_block_table = block_table;
+            c.app_bt_stride = p.bt_stride;
+            c.app_num_pages = p.num_pages;
+            c.app_scale_log2 = p.scale_log2;
+        }
         if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s, comb_ev) != hipSuccess) {
             return PKV_ELAUNCH;
         }
@@ -557,6 +603,24 @@ pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
     pkv_decode_desc a = *d;
     a.max_seqlen = d->max_seqlen > 0 ? d->max_seqlen + seqlen_new : 0;
     return a;
+}
+
+// The one-token append folds into the combine for one query token, 16-bit
+// caches, no window or ALiBi (a causal mask changes nothing for one query
+// token), on the tile schedule with the row-per-wave
+// combine (a few parts per stream): then the partition attends the cached
+// tokens, the combine adds the new one and stores it, and no append kernel
+// runs.  Other calls append first and then attend the longer rows.
+bool fold_fits(const Resolved& r, const pkv_decode_desc* d, int num_splits, int64_t seqlen_new) {
+    if (seqlen_new != 1 || r.multi_query || r.kv_fp8) {
+        return false;
+    }
+    const SplitPlan plan = resolve_splits(d, r, num_splits);
+    if (plan.schedule != PKV_SCHED_TILES) {
+        return false;
+    }
+    const CombineForm f = combine_form(r, plan);
+    return !f.by_stream && !f.long_rows && !f.row_groups;
 }
 
 } // namespace
@@ -716,6 +780,15 @@ size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_spl
     return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + pkv_decode_workspace_size(&a, num_splits);
 }
 
+int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new) {
+    Resolved r;
+    if (resolve(desc, r) != PKV_OK || seqlen_new < 0 || num_splits < 0) {
+        return -1;
+    }
+    const pkv_decode_desc a = appended_desc(desc, seqlen_new);
+    return fold_fits(r, &a, num_splits, seqlen_new) ? 1 : 0;
+}
+
 int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                       const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_new,
                       float softmax_scale, int num_splits, void* out, const pkv_decode_desc* desc, void* stream) {
@@ -747,6 +820,14 @@ int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void*
     if (pkv_decode_workspace_size(&a, num_splits) == 0) {
         a.workspace = nullptr;
         a.workspace_bytes = 0;
+    }
+    // One new token on the common decode shape: the partition attends the
+    // cached tokens and the combine adds the new one and stores it (two
+    // launches instead of three; the lengths region stays unused).
+    if (fold_fits(r, &a, num_splits, seqlen_new)) {
+        const AppendFold fold{k_new, v_new, k_cache, v_cache};
+        return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, &a,
+                           stream, true, &fold);
     }
     // Every check of the attention runs before the cache is written.
     st = decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, false);

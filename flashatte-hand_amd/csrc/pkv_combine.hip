@@ -302,13 +302,98 @@ __device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
     return t;
 }
 
+// Row (b, h) of a decode with a one-token append (p.app_k set): the
+// partition attended the row's cache_seqlens[b] cached tokens and left every
+// stream's parts in partial slots (force_partial); the new token j = L (its
+// position) joins them here as one more part of weight exp2(s - max), s the
+// log2-domain score q . k_new, with value v_new.  Its K and V rows go to slot
+// L of the row's block table, written by the row of the first query head of
+// each KV head.  A position past the block-table row is neither written nor
+// attended (the append kernel skips it too); a page id outside
+// [0, num_pages) is not written, and the token is attended from k_new.
+template <bool BF16, int D, int kBatch>
+__device__ __forceinline__ void combine_append_row(const CombineParams& p, const TileRow& t, int row, int lane,
+                                                   uint16_t* dst) {
+    constexpr int E = D / 64;
+    const int h = row - t.b * p.num_heads;
+    const int hk = p.num_heads / p.group;
+    const int kvh = h / p.group;
+    const int64_t new_row = (static_cast<int64_t>(t.b) * hk + kvh) * D + lane * E;
+    // Loads that do not wait on cache_seqlens: q, k_new, v_new.
+    float qv[E], kv[E], vv[E];
+    uint16_t kb[E], vb[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint16_t qb = p.app_q[static_cast<int64_t>(row) * D + lane * E + e];
+        kb[e] = p.app_k[new_row + e];
+        vb[e] = p.app_v[new_row + e];
+        float a, b;
+        unpack2<BF16>(static_cast<uint32_t>(qb) | (static_cast<uint32_t>(kb[e]) << 16), a, b);
+        qv[e] = a;
+        kv[e] = b;
+        unpack2<BF16>(static_cast<uint32_t>(vb[e]), a, b);
+        vv[e] = a;
+    }
+    const int32_t L = clamped_seqlen(p.seqlens, t.b, p.row_cap);
+    const RowUnits ru = row_units(p, t.b, lane);
+    float mx = kNegInf;
+    float den = 0.f;
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        acc[e] = 0.f;
+    }
+    if (ru.nb > 0) {
+        const StreamParts sp = stream_parts(p, ru, t.b, t.u);
+        const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+        merge_parts<E, kBatch>(p.part_lse + sp.slot0 * p.part_heads + t.hn,
+                               p.part_o + (sp.slot0 * p.part_heads + t.hn) * D + lane * E, lse_stride,
+                               lse_stride * D, 0, sp.parts, lane, mx, den, acc);
+    }
+    const int32_t raw = p.seqlens[t.b];
+    const bool fits = uniform(max(raw, 0)) < p.row_cap;
+    if (fits) {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s = fmaf(qv[e], kv[e], s);
+        }
+        s = group_sum<64>(s) * p.app_scale_log2;
+        const float m2 = fmaxf(mx, s);
+        const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
+        const float w = fast_exp2(s - m2);
+        den = den * a + w;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            acc[e] = fmaf(w, vv[e], acc[e] * a);
+        }
+        if (h == kvh * p.group) {
+            const int32_t page = p.app_block_table[static_cast<int64_t>(t.b) * p.app_bt_stride + (L >> p.page_shift)];
+            if (page >= 0 && page < p.app_num_pages) {
+                const int64_t slot = (static_cast<int64_t>(page) << p.page_shift) | (L & ((1 << p.page_shift) - 1));
+                const int64_t at = (slot * hk + kvh) * D + lane * E;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    p.app_k_cache[at + e] = kb[e];
+                    p.app_v_cache[at + e] = vb[e];
+                }
+            }
+        }
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+}
+
 // Tile-balanced schedule: row (b, h) belongs to stream u of row b; its parts
 // are located by stream_parts.  One part means the partition already wrote
 // the row; a row without tokens gets zeros; otherwise the partials in slots
 // slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
 // at a time: 16, or for streams of many parts (long rows) as many as 128
 // registers hold, so such a row takes one round trip instead of several.
-template <bool BF16, int D, int kBatch>
+template <bool BF16, int D, int kBatch, bool APPEND = false>
 __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
     const int lane = threadIdx.x & 63;
@@ -318,6 +403,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     }
     const TileRow t = tile_row(p, row);
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
+    if constexpr (APPEND) {
+        combine_append_row<BF16, D, kBatch>(p, t, row, lane, dst);
+        return;
+    }
 
     const RowUnits ru = row_units(p, t.b, lane);
     if (ru.nb == 0) {
@@ -604,6 +693,8 @@ static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, c
     } else if (p.tile_workers > 0 && p.long_rows) {
         constexpr int kLong = 128 / (D / 64) < 64 ? 128 / (D / 64) : 64;
         launch_kernel(combine_tiles_kernel<BF16, D, kLong>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
+    } else if (p.tile_workers > 0 && p.app_k != nullptr) {
+        launch_kernel(combine_tiles_kernel<BF16, D, 16, true>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else if (p.tile_workers > 0) {
         launch_kernel(combine_tiles_kernel<BF16, D, 16>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else {

@@ -42,6 +42,8 @@ struct PartitionParams {
     int32_t tile_workers; // > 0: tile-balanced schedule with this many waves
     int32_t part_heads;   // rows per partial slot in the tile-balanced schedule
     int32_t gang_shift;   // tile-balanced schedule: 2^gang_shift waves of a workgroup share a unit share
+    int32_t force_partial; // tile-balanced schedule: a stream one worker covers whole still goes to a
+                           // partial slot (the combine adds an appended token to every row)
     float scale_log2;     // softmax_scale * log2(e)
     // Query rows: each KV head serves rows = q_len * group query rows,
     // r = i * group + g for query token i and head g of the group.  With
@@ -81,6 +83,20 @@ struct CombineParams {
     int32_t heads_per_wave; // query rows per stream (16 MFMA, 1/2/4 VALU)
     int32_t q_len;        // as in PartitionParams; rows = B * q_len * H
     int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
+    // Decode with a one-token append folded in (app_k != null; tile schedule, one
+    // query token, 16-bit caches, no mask): the partition attended the cached
+    // cache_seqlens[b] tokens and left a partial for every stream; the combine
+    // adds the new token (q . k_new, v_new) to each row and writes k_new / v_new
+    // ([B, 1, Hk, D]) into slot cache_seqlens[b] of the row's block table.
+    const uint16_t* app_q;
+    const uint16_t* app_k;
+    const uint16_t* app_v;
+    uint16_t* app_k_cache;
+    uint16_t* app_v_cache;
+    const int32_t* app_block_table;
+    int32_t app_bt_stride;
+    int32_t app_num_pages;
+    float app_scale_log2;
     int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
     int32_t long_rows;    // tile schedule, a row per wave: many parts per stream, all in one round trip
     int32_t row_groups;   // tile schedule, a workgroup per row: very many parts per stream (few long rows)

@@ -1229,7 +1229,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 typename Math::Acc acc;
                 attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc,
                                                         ks.score_log2);
-                if (t_lo == 0 && t_hi == nb) {
+                if (t_lo == 0 && t_hi == nb && !p.force_partial) {
                     Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
                 } else {
                     const int64_t slot =

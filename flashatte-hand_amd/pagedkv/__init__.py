@@ -175,6 +175,11 @@ def path_for(desc: PkvDecodeDesc) -> int:
     return int(_lib.load().pkv_decode_path(ctypes.byref(desc)))
 
 
+def append_folds(desc: PkvDecodeDesc, num_splits: int = 0, seqlen_new: int = 1) -> bool:
+    """Whether decode with k_new / v_new folds the append into the attention's two kernels."""
+    return int(_lib.load().pkv_decode_append_folds(ctypes.byref(desc), int(num_splits), int(seqlen_new))) == 1
+
+
 def _check_cuda(name, t):
     if not t.is_cuda:
         raise PkvError(PKV_EINVAL, f"{name} must be a device tensor")

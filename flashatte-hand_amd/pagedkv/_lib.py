@@ -55,6 +55,7 @@ EXPORTS = {
     "pkv_reshape_and_cache": (ctypes.c_int, None),
     "pkv_decode_append": (ctypes.c_int, None),
     "pkv_decode_append_workspace_size": (ctypes.c_size_t, None),
+    "pkv_decode_append_folds": (ctypes.c_int, None),
 }
 
 
@@ -151,6 +152,8 @@ def load() -> ctypes.CDLL:
     ]
     lib.pkv_decode_append_workspace_size.restype = ctypes.c_size_t
     lib.pkv_decode_append_workspace_size.argtypes = [desc_p, ctypes.c_int, ctypes.c_int64]
+    lib.pkv_decode_append_folds.restype = ctypes.c_int
+    lib.pkv_decode_append_folds.argtypes = [desc_p, ctypes.c_int, ctypes.c_int64]
     for name in ("pkv_strerror", "run_kernel", "pkv_last_status"):
         res, args = EXPORTS[name]
         fn = getattr(lib, name)

@@ -213,3 +213,119 @@ def test_decode_append_int_seqlens_and_zero_new_tokens(rng):
                                            block_table=i32(bt), softmax_scale=0.125)
     torch.cuda.synchronize()
     assert np.max(np.abs(po.bits_to_f32(from_dev(out0), dtype) - want)) < TOL[dtype]
+
+
+FOLD = [
+    # B, H, Hk, D, P, leading rows, other rows' base length, dtype, path
+    (12, 32, 8, 128, 64, [511, 0, 64, 63], 300, 1, 0),      # an empty row; new tokens opening and closing a page
+    (12, 8, 8, 64, 16, [17, 0, 300], 600, 0, 0),            # one query head per KV head, head_dim 64
+    (48, 16, 2, 256, 16, [100, 15], 600, 0, 0),             # head_dim 256
+    (12, 64, 8, 128, 32, [1, 2, 33, 95, 200], 600, 1, 0),   # eight query heads per KV head
+    (12, 32, 8, 128, 16, [40, 0, 3, 900], 300, 1, 1),       # VALU math
+]
+
+
+def fold_lens(lead, base, B):
+    """The leading rows' lengths, then ragged rows around `base` (long enough for the tile schedule)."""
+    return list(lead) + [base + (37 * i) % 101 for i in range(B - len(lead))]
+
+
+def fold_desc(pagedkv, B, H, Hk, D, P, kc, bt, dtype, path):
+    return pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P,
+                             num_pages=kc.shape[0], block_table_stride=bt.shape[1],
+                             dtype=pagedkv.PKV_DTYPE_F16 if dtype == 0 else pagedkv.PKV_DTYPE_BF16, path=path)
+
+
+@pytest.mark.parametrize("B,H,Hk,D,P,lead,base,dtype,path", FOLD)
+def test_decode_append_folded_matches_oracle(rng, B, H, Hk, D, P, lead, base, dtype, path):
+    """One new token per row on the tile schedule: the partition attends the cached tokens, the
+    combine adds the new one and stores it.  Caches bit-exact, output within the decode tolerance."""
+    import pagedkv
+
+    torch = torch_mod()
+    lens = fold_lens(lead, base, B)
+    announce("decode_append-folded", B, H, Hk, D, P, lead, base, dtype, "path", path)
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, lens=lens, n=1, dtype=dtype)
+    assert pagedkv.append_folds(fold_desc(pagedkv, B, H, Hk, D, P, kc, bt, dtype, path), 0, 1)
+    scale = 1.0 / math.sqrt(D)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    want = po.decode_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, 1), scale, dtype)
+    dk, dv, dsl = to_dev(kc, dtype), to_dev(vc, dtype), i32(sl)
+    out = pagedkv.decode(to_dev(q, dtype), dk, dv, i32(bt), dsl, scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype), path=path)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+    np.testing.assert_array_equal(dsl.cpu().numpy(), sl)
+    got = po.bits_to_f32(from_dev(out), dtype)
+    assert np.max(np.abs(got - want)) < TOL[dtype]
+    # A row that held no tokens attends only the new one: its V row, exactly.
+    for b in np.nonzero(np.asarray(lens) == 0)[0]:
+        heads = np.arange(H) // (H // Hk)
+        np.testing.assert_array_equal(from_dev(out)[b, 0], nv[b, 0, heads])
+
+
+def test_decode_append_folded_at_row_capacity(rng):
+    """Rows at the block table's capacity (24 pages of 16 = 384 tokens): 383 cached tokens take
+    the new one in the last slot; 384 (and a length past the capacity) keep their tokens, the
+    new token is neither stored nor attended."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("decode_append-folded-capacity")
+    B, H, Hk, D, P, dtype = 12, 32, 8, 128, 16, 1
+    stride = 24
+    pool = B * stride + 2
+    bt = rng.permutation(pool).astype(np.int32)[:B * stride].reshape(B, stride).copy()
+    sl = np.array(fold_lens([383, 384, 400], 200, B), dtype=np.int32)
+    q = rand_bits(rng, (B, 1, H, D), dtype)
+    kc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    vc = rand_bits(rng, (pool, P, Hk, D), dtype)
+    nk = rand_bits(rng, (B, 1, Hk, D), dtype)
+    nv = rand_bits(rng, (B, 1, Hk, D), dtype)
+    assert pagedkv.append_folds(fold_desc(pagedkv, B, H, Hk, D, P, kc, bt, dtype, 0), 0, 1)
+    scale = 1.0 / math.sqrt(D)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+    want = po.decode_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, 1), scale, dtype)
+    dk, dv = to_dev(kc, dtype), to_dev(vc, dtype)
+    out = pagedkv.decode(to_dev(q, dtype), dk, dv, i32(bt), i32(sl), scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(dk), want_k)
+    np.testing.assert_array_equal(from_dev(dv), want_v)
+    assert np.max(np.abs(po.bits_to_f32(from_dev(out), dtype) - want)) < TOL[dtype]
+
+
+@pytest.mark.parametrize("config", ["c2", "c5"])
+def test_decode_append_folded_full_size(config):
+    """Benchmark shapes at full size: the folded call against the append kernel followed by a
+    plain decode over the longer rows (both on the GPU): caches bit-exact, outputs within the
+    decode tolerance."""
+    import pagedkv
+    from pagedkv.configs import make_config, make_tensors
+
+    torch = torch_mod()
+    announce("decode_append-folded-full", config)
+    cfg = make_config(config)
+    t = make_tensors(cfg, "cuda")
+    dtype = 0 if cfg.dtype == "f16" else 1
+    prev = (t["cache_seqlens"] - 1).clamp(min=0).to(torch.int32).contiguous()
+    g = torch.Generator(device="cuda").manual_seed(cfg.seed)
+    shape = (cfg.batch, 1, cfg.num_heads_k, cfg.head_dim)
+    nk = torch.randn(shape, device="cuda", generator=g).to(t["k_cache"].dtype)
+    nv = torch.randn(shape, device="cuda", generator=g).to(t["k_cache"].dtype)
+    desc = pagedkv.make_desc(batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k,
+                             head_dim=cfg.head_dim, page_size=cfg.page_size, num_pages=t["k_cache"].shape[0],
+                             block_table_stride=cfg.block_table.shape[1],
+                             dtype=pagedkv.PKV_DTYPE_F16 if dtype == 0 else pagedkv.PKV_DTYPE_BF16)
+    assert pagedkv.append_folds(desc, 0, 1)
+    k1, v1 = t["k_cache"], t["v_cache"]
+    k2, v2 = k1.clone(), v1.clone()
+    one = pagedkv.decode(t["q"], k1, v1, t["block_table"], prev, cfg.scale, 0, k_new=nk, v_new=nv)
+    pagedkv.append_kv(nk, nv, k2, v2, t["block_table"], prev)
+    two = pagedkv.decode(t["q"], k2, v2, t["block_table"], t["cache_seqlens"], cfg.scale, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16))
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+    diff = (one.float() - two.float()).abs().max().item()
+    assert diff < TOL[dtype], diff
