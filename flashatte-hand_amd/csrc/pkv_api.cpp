@@ -113,6 +113,9 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if ((d->mask & PKV_MASK_WINDOW) != 0 && (d->window_left < -1 || d->window_right < -1)) {
         return PKV_EINVAL;
     }
+    if ((reinterpret_cast<uintptr_t>(d->softmax_lse) & 3u) != 0) {
+        return PKV_EINVAL;
+    }
     const int64_t M = std::max<int64_t>(1, d->seqlen_q);
     // 32-bit index limits of the kernels: item counts, page ids, rows of the block table.  Each
     // factor is bounded before the product, so no size overflows the check itself.
@@ -490,6 +493,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.kv_fp8 = r.kv_fp8 ? 1 : 0;
     p.k_scale = desc->k_scale;
     p.v_scale = desc->v_scale;
+    p.lse = desc->softmax_lse;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -531,6 +535,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.group = p.group;
         c.head_groups = p.head_groups;
         c.heads_per_wave = r.heads_per_wave;
+        c.lse = desc->softmax_lse;
         if (fold != nullptr) {
             c.app_q = p.q;
             c.app_k = static_cast<const uint16_t*>(fold->k_new);

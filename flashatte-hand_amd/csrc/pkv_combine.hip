@@ -147,6 +147,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_kernel(CombinePara
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(acc[e] * inv);
     }
+    if (p.lse != nullptr && lane == 0) {
+        store_lse(p.lse, row, p.q_len, p.num_heads, mx, den);
+    }
 }
 
 // Row b's tiles, and the stream units of the rows before b and of all rows
@@ -363,6 +366,7 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
         const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
         const float w = fast_exp2(s - m2);
         den = den * a + w;
+        mx = m2;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             acc[e] = fmaf(w, vv[e], acc[e] * a);
@@ -384,6 +388,9 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+    if (p.lse != nullptr && lane == 0) {
+        store_lse(p.lse, row, 1, p.num_heads, mx, den);
     }
 }
 
@@ -414,6 +421,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
         for (int e = 0; e < E; ++e) {
             dst[e] = 0;
         }
+        if (p.lse != nullptr && lane == 0) {
+            store_lse(p.lse, row, p.q_len, p.num_heads, 0.f, 0.f);
+        }
         return;
     }
     const StreamParts sp = stream_parts(p, ru, t.b, t.u);
@@ -431,6 +441,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+    if (p.lse != nullptr && lane == 0) {
+        store_lse(p.lse, row, p.q_len, p.num_heads, mx, den);
     }
 }
 
@@ -459,6 +472,9 @@ __global__ __launch_bounds__(64 * kRowGroupWaves) void combine_row_group_kernel(
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 dst[e] = 0;
+            }
+            if (p.lse != nullptr && lane == 0) {
+                store_lse(p.lse, row, p.q_len, p.num_heads, 0.f, 0.f);
             }
         }
         return;
@@ -516,6 +532,9 @@ __global__ __launch_bounds__(64 * kRowGroupWaves) void combine_row_group_kernel(
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(out[e] * inv);
     }
+    if (p.lse != nullptr && lane == 0) {
+        store_lse(p.lse, row, p.q_len, p.num_heads, m, tot);
+    }
 }
 
 // Tile-balanced schedule, few parts per stream: one wave per block of
@@ -565,6 +584,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 dst[e] = 0;
+            }
+            if (p.lse != nullptr && lane == 0) {
+                store_lse(p.lse, out_row(r), p.q_len, p.num_heads, 0.f, 0.f);
             }
         }
         return;
@@ -672,6 +694,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 dst[e] = from_f32<BF16>(acc[r][e] * inv);
+            }
+            if (p.lse != nullptr && lane == 0) {
+                store_lse(p.lse, out_row(r), p.q_len, p.num_heads, l0[r], d);
             }
         }
     }

@@ -59,6 +59,7 @@ struct PartitionParams {
     int32_t kv_fp8;
     const float* k_scale;
     const float* v_scale;
+    float* lse;           // optional fp32 [B, H, M]: natural-log LSE of each output row (store_lse)
 };
 
 struct CombineParams {
@@ -97,6 +98,7 @@ struct CombineParams {
     int32_t app_bt_stride;
     int32_t app_num_pages;
     float app_scale_log2;
+    float* lse;           // as in PartitionParams
     int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
     int32_t long_rows;    // tile schedule, a row per wave: many parts per stream, all in one round trip
     int32_t row_groups;   // tile schedule, a workgroup per row: very many parts per stream (few long rows)
@@ -220,6 +222,23 @@ __device__ __forceinline__ uint4 load_kv16(const uint16_t* ptr) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// flash-attn's softmax_lse ([B, H, M], natural log) of output row `row` of
+// [B, M, H]: (m2 + log2 l) * ln 2 from a log2-domain max m2 and the weight sum
+// l of the row's probabilities exp2(s - m2); +inf for a row that saw no key
+// (flash-attn 2.6.3 writes +inf there; mathematically log 0 = -inf).
+__device__ __forceinline__ void store_lse(float* lse, int64_t row, int32_t q_len, int32_t num_heads, float m2,
+                                          float l) {
+    int64_t at = row;
+    if (q_len > 1) {
+        const int64_t per_b = static_cast<int64_t>(q_len) * num_heads;
+        const int64_t b = row / per_b;
+        const int64_t rem = row - b * per_b;
+        const int64_t i = rem / num_heads;
+        at = (b * num_heads + (rem - i * num_heads)) * q_len + i;
+    }
+    lse[at] = l > 0.f ? (m2 + fast_log2(l)) * 0.69314718055994531f : __builtin_huge_valf();
+}
 
 // Dot product of two packed 16-bit pairs accumulated into fp32 (v_dot2c_f32_{bf16,f16}).
 template <bool BF16>

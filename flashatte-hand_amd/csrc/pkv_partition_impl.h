@@ -600,6 +600,9 @@ struct MfmaMath {
                     w.y = pack2<BF16>(a.o[nb][dt][2] * inv, a.o[nb][dt][3] * inv);
                     *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
                 }
+                if (p.lse != nullptr && j == 0) {
+                    store_lse(p.lse, row, p.q_len, p.num_heads, a.m[nb] - kProbLog2Offset, a.l[nb]);
+                }
             }
         }
     }
@@ -829,6 +832,9 @@ struct ValuMath {
                     w.x = pack2<BF16>(a.o[h][0] * inv, a.o[h][1] * inv);
                     w.y = pack2<BF16>(a.o[h][2] * inv, a.o[h][3] * inv);
                     *reinterpret_cast<uint2*>(dst) = w;
+                }
+                if (p.lse != nullptr && lane == 0) {
+                    store_lse(p.lse, bh_first + h, 1, p.num_heads, a.m[h], a.l[h]);
                 }
             }
         }
@@ -1065,6 +1071,9 @@ void partition_split_kernel(PartitionParams p) {
                 *reinterpret_cast<uint4*>(p.out + Math::out_row(p, b, kvh, r_first + g) * D + c * 8) =
                     make_uint4(0u, 0u, 0u, 0u);
             }
+            if (p.lse != nullptr && lane < heads_here) {
+                store_lse(p.lse, Math::out_row(p, b, kvh, r_first + lane), p.q_len, p.num_heads, 0.f, 0.f);
+            }
         }
         return;
     }
@@ -1122,6 +1131,9 @@ void partition_item_group_kernel(PartitionParams p) {
                 const int c = idx % CH;
                 *reinterpret_cast<uint4*>(p.out + Math::out_row(p, it.b, it.kvh, r_first + g) * D + c * 8) =
                     make_uint4(0u, 0u, 0u, 0u);
+            }
+            if (p.lse != nullptr && lane < heads_here) {
+                store_lse(p.lse, Math::out_row(p, it.b, it.kvh, r_first + lane), p.q_len, p.num_heads, 0.f, 0.f);
             }
         }
         return;

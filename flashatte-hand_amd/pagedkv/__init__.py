@@ -105,6 +105,7 @@ def make_desc(
     kv_dtype: int = PKV_KV_DTYPE_SAME,
     k_scale: int = 0,
     v_scale: int = 0,
+    softmax_lse: int = 0,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -131,6 +132,7 @@ def make_desc(
     d.alibi_batch_stride = alibi_batch_stride
     d.k_scale = k_scale or None
     d.v_scale = v_scale or None
+    d.softmax_lse = softmax_lse or None
     return d
 
 
@@ -210,8 +212,13 @@ def decode(
     alibi_slopes=None,
     k_scale=None,
     v_scale=None,
+    softmax_lse=None,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
+
+    ``softmax_lse``, an fp32 ``[B, H, M]`` device tensor, receives each query
+    row's log-sum-exp of its scaled scores (natural log; +inf for a row with no
+    visible key), as flash-attn's ``return_softmax_lse`` returns it.
 
     Caches of dtype ``torch.float8_e4m3fn`` are OCP FP8 e4m3 with optional fp32
     per-KV-head dequantisation scales ``k_scale`` / ``v_scale`` ([Hk]); the
@@ -261,6 +268,12 @@ def decode(
             raise PkvError(PKV_EINVAL, "out must match q")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(D)
+    lse_ptr = 0
+    if softmax_lse is not None:
+        _check_cuda("softmax_lse", softmax_lse)
+        if softmax_lse.dtype != torch.float32 or tuple(softmax_lse.shape) != (B, H, M):
+            raise PkvError(PKV_EINVAL, "softmax_lse must be fp32 [B, H, M]")
+        lse_ptr = softmax_lse.data_ptr()
     seqlen_new = 0
     if k_new is not None or v_new is not None:
         seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
@@ -272,6 +285,7 @@ def decode(
         split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
         alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride, kv_dtype=kv_dtype,
         k_scale=_scale_ptr("k_scale", k_scale, Hk), v_scale=_scale_ptr("v_scale", v_scale, Hk),
+        softmax_lse=lse_ptr,
     )
     lib = _lib.load()
     if seqlen_new:
@@ -420,9 +434,11 @@ def flash_attn_with_kvcache(
     ``cache_seqlens`` (a tensor or one int for every row); new tokens ``k`` /
     ``v`` [B, seqlen_new, Hk, D], written into the caches in place before the
     attention, which then covers ``cache_seqlens + seqlen_new`` tokens;
-    ``causal`` (bottom-right aligned), ``window_size`` and ``alibi_slopes``.
-    Rotary embedding, ``cache_batch_idx``, ``cache_leftpad``, ``softcap`` and
-    ``return_softmax_lse`` raise PkvError(PKV_EUNSUPPORTED).
+    ``causal`` (bottom-right aligned), ``window_size`` and ``alibi_slopes``;
+    ``return_softmax_lse`` returns ``(out, softmax_lse)`` with softmax_lse fp32
+    ``[B, H, M]`` (natural log, +inf for a row with no visible key).
+    Rotary embedding, ``cache_batch_idx``, ``cache_leftpad`` and ``softcap``
+    raise PkvError(PKV_EUNSUPPORTED).
     """
     if rotary_cos is not None or rotary_sin is not None:
         raise PkvError(PKV_EUNSUPPORTED, "rotary embedding of the new K")
@@ -430,8 +446,6 @@ def flash_attn_with_kvcache(
         raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
     if softcap:
         raise PkvError(PKV_EUNSUPPORTED, "softcap")
-    if return_softmax_lse:
-        raise PkvError(PKV_EUNSUPPORTED, "return_softmax_lse")
     if block_table is None or cache_seqlens is None:
         raise PkvError(PKV_EUNSUPPORTED, "only the paged layout (block_table + cache_seqlens) is implemented")
     if isinstance(cache_seqlens, int):
@@ -441,9 +455,14 @@ def flash_attn_with_kvcache(
         k = k.contiguous()
     if v is not None:
         v = v.contiguous()
-    return decode(q.contiguous(), k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k,
-                  v_new=v, causal=causal, window_size=window_size,
-                  alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous())
+    lse = None
+    if return_softmax_lse:
+        torch = _torch()
+        lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device)
+    out = decode(q.contiguous(), k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k,
+                 v_new=v, causal=causal, window_size=window_size,
+                 alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous(), softmax_lse=lse)
+    return (out, lse) if return_softmax_lse else out
 
 
 def run_kernel(

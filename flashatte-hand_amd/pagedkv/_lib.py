@@ -87,6 +87,7 @@ class PkvDecodeDesc(ctypes.Structure):
         ("alibi_batch_stride", ctypes.c_int64),
         ("k_scale", ctypes.c_void_p),
         ("v_scale", ctypes.c_void_p),
+        ("softmax_lse", ctypes.c_void_p),
     ]
 
 

@@ -105,6 +105,10 @@ typedef struct pkv_decode_desc {
     const float* k_scale;       /* FP8 caches: optional fp32 [Hk] device array, K = fp8 * k_scale[kv head];
                                    NULL = 1.  The append divides by it before rounding to FP8. */
     const float* v_scale;       /* FP8 caches: the same for V */
+    float* softmax_lse;         /* optional fp32 [B, H, M] device array (flash-attn's return_softmax_lse):
+                                   log(sum_j exp(softmax_scale * q . k_j + bias_j)) over the keys each
+                                   query row attends, natural log; +inf for a row with no visible key
+                                   (flash-attn 2.6.3's convention).  NULL = not written. */
 } pkv_decode_desc;
 
 /*

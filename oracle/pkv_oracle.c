@@ -390,7 +390,7 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
                           const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_q, int causal,
                           int64_t window_left, int64_t window_right, const float* alibi_slopes,
                           int64_t alibi_batch_stride, int kv_fp8, const float* k_scale, const float* v_scale,
-                          double softmax_scale, double* out) {
+                          double softmax_scale, double* out, double* lse) {
     build_f16_table();
     set_threads(d);
     const int64_t B = d->batch, H = d->num_heads, D = d->head_dim, M = seqlen_q;
@@ -420,6 +420,11 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
             const double ks = (kv_fp8 && k_scale) ? (double)k_scale[kvh] : 1.0;
             const double vs = (kv_fp8 && v_scale) ? (double)v_scale[kvh] : 1.0;
             double* o = out + row * D;
+            /* softmax_lse [B, H, M]: +inf until a visible key sets it (flash-attn's empty-row value) */
+            double* l = lse ? lse + (b * H + h) * M + i : NULL;
+            if (l) {
+                *l = INFINITY;
+            }
             for (int64_t c = 0; c < D; ++c) {
                 o[c] = 0.0;
                 acc[c] = 0.0;
@@ -471,6 +476,9 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
             for (int64_t c = 0; c < D; ++c) {
                 o[c] = acc[c] / denom;
             }
+            if (l) {
+                *l = mx + log(denom);
+            }
         }
         free(scores);
         free(qd);
@@ -481,18 +489,18 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                          const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out) {
+                         double* out, double* lse) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out);
+                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out, lse);
 }
 
 void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint8_t* k_cache,
                           const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                           int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                           const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
-                          const float* v_scale, double softmax_scale, double* out) {
+                          const float* v_scale, double softmax_scale, double* out, double* lse) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out);
+                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out, lse);
 }
 
 /* ---------------------------------------------------------------- split-KV algebra */

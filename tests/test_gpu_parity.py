@@ -330,20 +330,28 @@ def test_baseline_config_full_size(name):
     t = make_tensors(cfg, "cuda")
     dt = 0 if cfg.dtype == "f16" else 1
     outs = {}
+    lses = {}
     for path in PATHS:
         for splits in sorted({cfg.num_splits, 1}):
             announce("config", name, "path", path, "splits", splits)
+            lse = torch.empty((cfg.batch, cfg.num_heads, 1), dtype=torch.float32, device="cuda")
             o = pagedkv.decode(t["q"], t["k_cache"], t["v_cache"], t["block_table"], t["cache_seqlens"], cfg.scale,
-                               splits, max_seqlen=int(cfg.seqlens.max()), path=path)
+                               splits, max_seqlen=int(cfg.seqlens.max()), path=path, softmax_lse=lse)
             torch.cuda.synchronize()
             outs[(path, splits)] = po.bits_to_f32(from_dev(o), dt)
+            lses[(path, splits)] = lse.cpu().numpy().astype(np.float64)
     for o in outs.values():
         assert np.isfinite(o).all()
     q = from_dev(t["q"])
     k = from_dev(t["k_cache"])
     v = from_dev(t["v_cache"])
     announce("config", name, "fp64 oracle over all", cfg.batch * cfg.num_heads, "rows")
-    want = po.decode_f64(q, k, v, cfg.block_table, cfg.seqlens, cfg.scale, dt)
+    want, want_lse = po.attn_f64(q, k, v, cfg.block_table, cfg.seqlens, cfg.scale, dt, lse=True)
+    for key, lse in lses.items():
+        # softmax_lse beside the output (flash-attn's return_softmax_lse); no row is empty here
+        assert np.isfinite(want_lse).all() and np.isfinite(lse).all(), key
+        lse_err = float(np.max(np.abs(lse - want_lse) / (5e-4 + 1e-5 * np.abs(want_lse))))
+        assert lse_err < 1.0, (key, lse_err)
     for key, o in outs.items():
         err = float(np.max(np.abs(o - want)))
         row_err = np.max(np.abs(o - want), axis=-1)  # [B, 1, H]
