@@ -50,6 +50,7 @@ struct Resolved {
     int head_groups;
     int path;
     int64_t max_pages;
+    bool rotary;      // rotary_cos / rotary_sin set (pkv_decode_append only)
 };
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -114,6 +115,19 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
         return PKV_EINVAL;
     }
     if ((reinterpret_cast<uintptr_t>(d->softmax_lse) & 3u) != 0) {
+        return PKV_EINVAL;
+    }
+    // Rotary tables: both or neither; rotary_dim a multiple of 16 within the
+    // head; at least one row per position a block-table row addresses
+    // (flash-attn 2.6.3 asks seqlen_ro >= seqlen_k of the cache).
+    r.rotary = d->rotary_cos != nullptr || d->rotary_sin != nullptr;
+    if (r.rotary &&
+        (d->rotary_cos == nullptr || d->rotary_sin == nullptr || d->rotary_dim < 16 || d->rotary_dim % 16 != 0 ||
+         d->rotary_dim > d->head_dim || (d->rotary_interleaved != 0 && d->rotary_interleaved != 1) ||
+         d->block_table_stride < 0 || d->page_size < 0 ||
+         d->rotary_seqlen < std::max<int64_t>(1, d->block_table_stride * d->page_size) ||
+         (reinterpret_cast<uintptr_t>(d->rotary_cos) & 1u) != 0 ||
+         (reinterpret_cast<uintptr_t>(d->rotary_sin) & 1u) != 0)) {
         return PKV_EINVAL;
     }
     const int64_t M = std::max<int64_t>(1, d->seqlen_q);
@@ -312,6 +326,12 @@ size_t workspace_bytes(const Resolved& r, const SplitPlan& plan) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rotary tables apply to appended keys: only pkv_decode_append takes them
+// (flash-attn 2.6.3 requires new keys when rotary_cos is given).
+bool rotary_set(const pkv_decode_desc* d) {
+    return d != nullptr && (d->rotary_cos != nullptr || d->rotary_sin != nullptr);
+}
 
 thread_local int t_last_status = PKV_OK;
 
@@ -604,6 +624,11 @@ pkv::LaunchEvents append_events(const pkv_decode_desc* d) {
 
 // Workspace of pkv_decode_append: the per-row lengths after the append, then
 // the attention's own workspace for the longer rows.
+// Workspace of pkv_decode_append with rotary tables: the rotated q ([B, M, H, D], 16-bit).
+size_t rotary_q_bytes(const Resolved& r) {
+    return r.rotary ? align_up(static_cast<size_t>(r.B * r.M * r.H * r.D) * sizeof(uint16_t)) : 0;
+}
+
 pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
     pkv_decode_desc a = *d;
     a.max_seqlen = d->max_seqlen > 0 ? d->max_seqlen + seqlen_new : 0;
@@ -617,7 +642,7 @@ pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
 // tokens, the combine adds the new one and stores it, and no append kernel
 // runs.  Other calls append first and then attend the longer rows.
 bool fold_fits(const Resolved& r, const pkv_decode_desc* d, int num_splits, int64_t seqlen_new) {
-    if (seqlen_new != 1 || r.multi_query || r.kv_fp8) {
+    if (seqlen_new != 1 || r.multi_query || r.kv_fp8 || r.rotary) {
         return false;
     }
     const SplitPlan plan = resolve_splits(d, r, num_splits);
@@ -686,6 +711,9 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
 int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
                const pkv_decode_desc* desc, void* stream) {
+    if (rotary_set(desc)) {
+        return PKV_EINVAL;
+    }
     return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, desc, stream,
                        true);
 }
@@ -693,7 +721,7 @@ int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const in
 int pkv_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
                        const int32_t* cache_seqlens, float softmax_scale, int num_splits, void* out,
                        const pkv_decode_desc* desc, void* stream) {
-    if (desc == nullptr) {
+    if (desc == nullptr || rotary_set(desc)) {
         return PKV_EINVAL;
     }
     // The size check is host arithmetic: an oversized plan fails before the device is touched.
@@ -719,6 +747,9 @@ int pkv_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, 
 
 int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache, const int32_t* block_table,
                   const int32_t* cache_seqlens, int64_t seqlen_new, const pkv_decode_desc* desc, void* stream) {
+    if (rotary_set(desc)) {
+        return PKV_EINVAL;
+    }
     Resolved r;
     const int st = resolve(desc, r);
     if (st != PKV_OK) {
@@ -743,7 +774,7 @@ int pkv_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_c
 int pkv_reshape_and_cache(const void* key, const void* value, void* k_cache, void* v_cache,
                           const int64_t* slot_mapping, int64_t num_tokens, const pkv_decode_desc* desc,
                           void* stream) {
-    if (desc == nullptr) {
+    if (desc == nullptr || rotary_set(desc)) {
         return PKV_EINVAL;
     }
     // Only the cache geometry matters here: the row-shaped fields get
@@ -782,7 +813,8 @@ size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_spl
         return pkv_decode_workspace_size(desc, num_splits);
     }
     const pkv_decode_desc a = appended_desc(desc, seqlen_new);
-    return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + pkv_decode_workspace_size(&a, num_splits);
+    return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + rotary_q_bytes(r) +
+           pkv_decode_workspace_size(&a, num_splits);
 }
 
 int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new) {
@@ -797,7 +829,7 @@ int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t
 int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
                       const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_new,
                       float softmax_scale, int num_splits, void* out, const pkv_decode_desc* desc, void* stream) {
-    if (seqlen_new == 0) {
+    if (seqlen_new == 0) { // with rotary tables pkv_decode refuses: they need new keys
         return pkv_decode(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, desc,
                           stream);
     }
@@ -813,15 +845,17 @@ int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void*
     if (!append_fits(r, seqlen_new)) {
         return PKV_EUNSUPPORTED;
     }
-    // The per-row lengths lead the workspace; the attention's partials follow.
+    // The per-row lengths lead the workspace, then (rotary) the rotated q;
+    // the attention's partials follow.
     const size_t lens_bytes = align_up(static_cast<size_t>(r.B) * sizeof(int32_t));
-    if (desc->workspace == nullptr || desc->workspace_bytes < lens_bytes || !aligned16(desc->workspace)) {
+    const size_t head_bytes = lens_bytes + rotary_q_bytes(r);
+    if (desc->workspace == nullptr || desc->workspace_bytes < head_bytes || !aligned16(desc->workspace)) {
         return PKV_ENOWORKSPACE;
     }
     int32_t* lens = static_cast<int32_t*>(desc->workspace);
     pkv_decode_desc a = appended_desc(desc, seqlen_new);
-    a.workspace = static_cast<char*>(desc->workspace) + lens_bytes;
-    a.workspace_bytes = desc->workspace_bytes - lens_bytes;
+    a.workspace = static_cast<char*>(desc->workspace) + head_bytes;
+    a.workspace_bytes = desc->workspace_bytes - head_bytes;
     if (pkv_decode_workspace_size(&a, num_splits) == 0) {
         a.workspace = nullptr;
         a.workspace_bytes = 0;
@@ -844,10 +878,33 @@ int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void*
     ap.seqlens = cache_seqlens;
     ap.seqlens_out = lens;
     ap.n_new = static_cast<int32_t>(seqlen_new);
-    if (pkv::launch_append(ap, static_cast<hipStream_t>(stream), {}) != hipSuccess) {
+    if (!r.rotary) {
+        if (pkv::launch_append(ap, static_cast<hipStream_t>(stream), {}) != hipSuccess) {
+            return PKV_ELAUNCH;
+        }
+        return decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, true);
+    }
+    // Rotary: one launch rotates and stores the new keys (V as is) and writes
+    // the rotated q into the workspace; the attention reads that q.
+    pkv::RotaryAppendParams rp{};
+    rp.a = ap;
+    rp.cos = static_cast<const uint16_t*>(desc->rotary_cos);
+    rp.sin = static_cast<const uint16_t*>(desc->rotary_sin);
+    rp.q = static_cast<const uint16_t*>(q);
+    rp.q_out = reinterpret_cast<uint16_t*>(static_cast<char*>(desc->workspace) + lens_bytes);
+    rp.rotary_seqlen = desc->rotary_seqlen;
+    rp.rotary_dim = desc->rotary_dim;
+    rp.interleaved = desc->rotary_interleaved;
+    rp.q_len = static_cast<int32_t>(r.M);
+    rp.num_heads = static_cast<int32_t>(r.H);
+    // flash-attn 2.6.3: queries sit at successive positions when the call is causal or local.
+    const bool local = (desc->mask & PKV_MASK_WINDOW) != 0 && (desc->window_left >= 0 || desc->window_right >= 0);
+    rp.q_positions = (desc->mask & PKV_MASK_CAUSAL) != 0 || local ? 1 : 0;
+    if (pkv::launch_rotary_append(rp, static_cast<hipStream_t>(stream)) != hipSuccess) {
         return PKV_ELAUNCH;
     }
-    return decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, true);
+    return decode_impl(rp.q_out, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream,
+                       true);
 }
 
 void run_kernel(const void* q, const void* k_cache_paged, const void* v_cache_paged, void* output,

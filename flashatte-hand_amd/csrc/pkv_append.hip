@@ -154,6 +154,179 @@ __global__ __launch_bounds__(kAppendThreads) void append_kernel(AppendParams p) 
     }
 }
 
+// ---------------------------------------------------------------- rotary embedding
+
+// One rotary pair in fp32, every product and sum rounded on its own (no fused
+// multiply-add): the IEEE single-precision value of (x0 c - x1 s, x0 s + x1 c).
+__device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float s) {
+#pragma clang fp contract(off)
+    const float y0 = x0 * c - x1 * s;
+    const float y1 = x0 * s + x1 * c;
+    x0 = y0;
+    x1 = y1;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void unpack8(const u32x4& w, float (&f)[8]) {
+    unpack2<BF16>(w.x, f[0], f[1]);
+    unpack2<BF16>(w.y, f[2], f[3]);
+    unpack2<BF16>(w.z, f[4], f[5]);
+    unpack2<BF16>(w.w, f[6], f[7]);
+}
+
+template <bool BF16>
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+    u32x4 w;
+    w.x = pack2<BF16>(f[0], f[1]);
+    w.y = pack2<BF16>(f[2], f[3]);
+    w.z = pack2<BF16>(f[4], f[5]);
+    w.w = pack2<BF16>(f[6], f[7]);
+    return w;
+}
+
+template <bool BF16>
+__device__ __forceinline__ float elem_f32(uint16_t v) {
+    return BF16 ? bf16_lo(v) : f16_lo(v);
+}
+
+// Chunk cc of one head row (`row`: its D / 8 chunks) rotated at position pos:
+// out[0] is chunk cc; with GPT-NeoX pairs a chunk in the first half of the
+// rotated dims (cc < rotary_dim / 16) also yields out[1], its partner chunk
+// cc + rotary_dim / 16.  Returns the chunks the caller stores: 1, 2, or 0 for
+// a partner chunk (its owner stores it).  Chunks past rotary_dim are copied.
+template <bool BF16>
+__device__ __forceinline__ int rotary_chunks(const RotaryAppendParams& p, const u32x4* row, int32_t cc, int64_t pos,
+                                             u32x4 (&out)[2]) {
+    const int32_t rd = p.rotary_dim;
+    if (8 * cc >= rd) {
+        out[0] = row[cc];
+        return 1;
+    }
+    const int64_t at = min(max(pos, int64_t{0}), p.rotary_seqlen - 1) * (rd / 2);
+    if (p.interleaved) {
+        float f[8];
+        unpack8<BF16>(row[cc], f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t k = at + 4 * cc + e; // pair (8 cc + 2 e, 8 cc + 2 e + 1)
+            rotate_pair(f[2 * e], f[2 * e + 1], elem_f32<BF16>(p.cos[k]), elem_f32<BF16>(p.sin[k]));
+        }
+        out[0] = pack8<BF16>(f);
+        return 1;
+    }
+    const int32_t half = rd / 16;
+    if (cc >= half) {
+        return 0;
+    }
+    float f0[8];
+    float f1[8];
+    unpack8<BF16>(row[cc], f0);
+    unpack8<BF16>(row[cc + half], f1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t k = at + 8 * cc + e; // pair (8 cc + e, 8 cc + e + rotary_dim / 2)
+        rotate_pair(f0[e], f1[e], elem_f32<BF16>(p.cos[k]), elem_f32<BF16>(p.sin[k]));
+    }
+    out[0] = pack8<BF16>(f0);
+    out[1] = pack8<BF16>(f1);
+    return 2;
+}
+
+// Items [0, tokens * chunks): a 16-byte chunk of a new token's K (rotated) and
+// V, stored at its block-table slot (and the row's new length, once per row);
+// then [.., + B * M * H * D / 8): a chunk of q, rotated into q_out.
+template <bool FP8, bool BF16>
+__global__ __launch_bounds__(kAppendThreads) void rotary_append_kernel(RotaryAppendParams p) {
+    const AppendParams& a = p.a;
+    const int32_t hc = a.head_chunks;
+    const int32_t half = p.rotary_dim / 16;
+    const int64_t k_items = a.tokens * a.chunks;
+    const int64_t q_rows = static_cast<int64_t>(a.batch) * p.q_len * p.num_heads;
+    const int64_t total = k_items + q_rows * hc;
+    const u32x4* k_new = reinterpret_cast<const u32x4*>(a.k_new);
+    const u32x4* v_new = reinterpret_cast<const u32x4*>(a.v_new);
+    for (int64_t x = static_cast<int64_t>(blockIdx.x) * kAppendThreads + threadIdx.x; x < total;
+         x += static_cast<int64_t>(gridDim.x) * kAppendThreads) {
+        if (x < k_items) {
+            const int64_t dst = append_dst<false>(a, x);
+            if (dst < 0) {
+                continue;
+            }
+            const int64_t i = x / a.chunks;
+            const int32_t c = static_cast<int32_t>(x - i * a.chunks);
+            const int32_t cc = c % hc;
+            const int32_t b = static_cast<int32_t>(i / a.n_new);
+            const int64_t pos = static_cast<int64_t>(max(a.seqlens[b], 0)) + (i - static_cast<int64_t>(b) * a.n_new);
+            u32x4 kr[2];
+            const int n = rotary_chunks<BF16>(p, k_new + (x - cc), cc, pos, kr);
+            const u32x4 vx = v_new[x];
+            if constexpr (FP8) {
+                uint2* k8 = reinterpret_cast<uint2*>(a.k_cache);
+                uint2* v8 = reinterpret_cast<uint2*>(a.v_cache);
+                const float ik = inv_scale(a.k_scale, c, hc);
+                if (n >= 1) {
+                    k8[dst] = quantize8<BF16>(kr[0], ik);
+                }
+                if (n == 2) {
+                    k8[dst + half] = quantize8<BF16>(kr[1], ik);
+                }
+                v8[dst] = quantize8<BF16>(vx, inv_scale(a.v_scale, c, hc));
+            } else {
+                u32x4* kc = reinterpret_cast<u32x4*>(a.k_cache);
+                u32x4* vc = reinterpret_cast<u32x4*>(a.v_cache);
+                if (n >= 1) {
+                    kc[dst] = kr[0];
+                }
+                if (n == 2) {
+                    kc[dst + half] = kr[1];
+                }
+                vc[dst] = vx;
+            }
+        } else {
+            const int64_t y = x - k_items;
+            const int64_t r = y / hc; // q row (b, i, h) of [B, M, H]
+            const int32_t cc = static_cast<int32_t>(y - r * hc);
+            const int64_t per_b = static_cast<int64_t>(p.q_len) * p.num_heads;
+            const int64_t b = r / per_b;
+            const int64_t i = (r - b * per_b) / p.num_heads;
+            const int64_t pos = static_cast<int64_t>(max(a.seqlens[b], 0)) + (p.q_positions ? i : 0);
+            u32x4 qr[2];
+            const int n = rotary_chunks<BF16>(p, reinterpret_cast<const u32x4*>(p.q) + r * hc, cc, pos, qr);
+            u32x4* orow = reinterpret_cast<u32x4*>(p.q_out) + r * hc;
+            if (n >= 1) {
+                orow[cc] = qr[0];
+            }
+            if (n == 2) {
+                orow[cc + half] = qr[1];
+            }
+        }
+    }
+}
+
+hipError_t launch_rotary_append(const RotaryAppendParams& p, hipStream_t stream) {
+    const int64_t total = p.a.tokens * p.a.chunks +
+                          static_cast<int64_t>(p.a.batch) * p.q_len * p.num_heads * p.a.head_chunks;
+    if (total <= 0) {
+        return hipSuccess;
+    }
+    const dim3 grid(static_cast<uint32_t>(std::min<int64_t>((total + kAppendThreads - 1) / kAppendThreads,
+                                                            kAppendMaxGroups)));
+    const dim3 block(kAppendThreads);
+    const LaunchEvents none{};
+    if (p.a.kv_fp8) {
+        if (p.a.bf16) {
+            launch_kernel(rotary_append_kernel<true, true>, grid, block, 0, stream, none, p);
+        } else {
+            launch_kernel(rotary_append_kernel<true, false>, grid, block, 0, stream, none, p);
+        }
+    } else if (p.a.bf16) {
+        launch_kernel(rotary_append_kernel<false, true>, grid, block, 0, stream, none, p);
+    } else {
+        launch_kernel(rotary_append_kernel<false, false>, grid, block, 0, stream, none, p);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_append(const AppendParams& p, hipStream_t stream, const LaunchEvents& ev) {
     const int64_t total = p.tokens * p.chunks;
     if (total <= 0) {

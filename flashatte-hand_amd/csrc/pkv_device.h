@@ -137,6 +137,28 @@ struct AppendParams {
     const float* v_scale;
 };
 
+// Block-table append with flash-attn's rotary embedding (flash_attn_with_kvcache
+// with rotary_cos / rotary_sin): new token j of row b is rotated at position
+// max(seqlens[b], 0) + j before it is stored; V is stored unrotated; q is
+// rotated into q_out at max(seqlens[b], 0) + i for query i (q_positions == 1,
+// causal or windowed calls) or at max(seqlens[b], 0) for every query.  Pair
+// (x0, x1) of angle index a becomes (x0 cos_a - x1 sin_a, x0 sin_a + x1 cos_a)
+// in fp32 without fused multiply-adds, rounded to the input dtype; the
+// dims from rotary_dim on are copied.
+struct RotaryAppendParams {
+    AppendParams a;               // block-table form, 16-bit new K / V
+    const uint16_t* cos;          // [rotary_seqlen, rotary_dim / 2], the input dtype
+    const uint16_t* sin;
+    const uint16_t* q;            // [B, M, H, D]
+    uint16_t* q_out;              // [B, M, H, D]: q rotated
+    int64_t rotary_seqlen;        // rows of cos / sin; positions past the last row use it
+    int32_t rotary_dim;           // multiple of 16, <= D
+    int32_t interleaved;          // 1: pairs (2p, 2p + 1); 0: (p, p + rotary_dim / 2) (GPT-NeoX)
+    int32_t q_len;                // M
+    int32_t num_heads;            // H
+    int32_t q_positions;
+};
+
 constexpr float kNegInf = -__builtin_huge_valf();
 
 // ---------------------------------------------------------------- 16-bit <-> fp32

@@ -44,4 +44,8 @@ hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipSt
 // the block-table form.
 hipError_t launch_append(const AppendParams& p, hipStream_t stream, const LaunchEvents& ev);
 
+// Block-table append with rotary embedding of the new keys, and q rotated
+// into p.q_out (RotaryAppendParams).
+hipError_t launch_rotary_append(const RotaryAppendParams& p, hipStream_t stream);
+
 } // namespace pkv

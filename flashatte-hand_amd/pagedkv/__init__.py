@@ -106,6 +106,11 @@ def make_desc(
     k_scale: int = 0,
     v_scale: int = 0,
     softmax_lse: int = 0,
+    rotary_cos: int = 0,
+    rotary_sin: int = 0,
+    rotary_seqlen: int = 0,
+    rotary_dim: int = 0,
+    rotary_interleaved: bool = True,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -133,6 +138,11 @@ def make_desc(
     d.k_scale = k_scale or None
     d.v_scale = v_scale or None
     d.softmax_lse = softmax_lse or None
+    d.rotary_cos = rotary_cos or None
+    d.rotary_sin = rotary_sin or None
+    d.rotary_seqlen = rotary_seqlen
+    d.rotary_dim = rotary_dim
+    d.rotary_interleaved = 1 if rotary_interleaved else 0
     return d
 
 
@@ -213,8 +223,16 @@ def decode(
     k_scale=None,
     v_scale=None,
     softmax_lse=None,
+    rotary_cos=None,
+    rotary_sin=None,
+    rotary_interleaved: bool = True,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
+
+    ``rotary_cos`` / ``rotary_sin`` ([seqlen_ro, rotary_dim / 2], q's dtype;
+    with ``k_new``) rotate the new keys at their positions before they are
+    stored and q at its positions (flash-attn 2.6.3's rotary embedding;
+    ``rotary_interleaved`` pairs dims (2a, 2a + 1), else (a, a + rotary_dim / 2)).
 
     ``softmax_lse``, an fp32 ``[B, H, M]`` device tensor, receives each query
     row's log-sum-exp of its scaled scores (natural log; +inf for a row with no
@@ -279,13 +297,24 @@ def decode(
         seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
         if k_new.dtype != q.dtype:
             raise PkvError(PKV_EINVAL, "k / v must have q's dtype")
+    rot = {}
+    if rotary_cos is not None or rotary_sin is not None:
+        if rotary_cos is None or rotary_sin is None or not seqlen_new:
+            raise PkvError(PKV_EINVAL, "rotary_cos and rotary_sin go together, with new keys k / v")
+        for name, t in (("rotary_cos", rotary_cos), ("rotary_sin", rotary_sin)):
+            _check_cuda(name, t)
+            if t.dtype != q.dtype or t.dim() != 2 or tuple(t.shape) != tuple(rotary_cos.shape):
+                raise PkvError(PKV_EINVAL, f"{name} must be [seqlen_ro, rotary_dim / 2] in q's dtype")
+        rot = dict(rotary_cos=rotary_cos.data_ptr(), rotary_sin=rotary_sin.data_ptr(),
+                   rotary_seqlen=rotary_cos.shape[0], rotary_dim=2 * rotary_cos.shape[1],
+                   rotary_interleaved=rotary_interleaved)
     desc = make_desc(
         batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=num_pages,
         block_table_stride=block_table.shape[1], dtype=_dtype_code(q.dtype), max_seqlen=max_seqlen, path=path,
         split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
         alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride, kv_dtype=kv_dtype,
         k_scale=_scale_ptr("k_scale", k_scale, Hk), v_scale=_scale_ptr("v_scale", v_scale, Hk),
-        softmax_lse=lse_ptr,
+        softmax_lse=lse_ptr, **rot,
     )
     lib = _lib.load()
     if seqlen_new:
@@ -436,12 +465,11 @@ def flash_attn_with_kvcache(
     attention, which then covers ``cache_seqlens + seqlen_new`` tokens;
     ``causal`` (bottom-right aligned), ``window_size`` and ``alibi_slopes``;
     ``return_softmax_lse`` returns ``(out, softmax_lse)`` with softmax_lse fp32
-    ``[B, H, M]`` (natural log, +inf for a row with no visible key).
-    Rotary embedding, ``cache_batch_idx``, ``cache_leftpad`` and ``softcap``
-    raise PkvError(PKV_EUNSUPPORTED).
+    ``[B, H, M]`` (natural log, +inf for a row with no visible key);
+    ``rotary_cos`` / ``rotary_sin`` with ``k`` / ``v`` rotate the new keys and
+    q (``rotary_interleaved`` as in flash-attn).  ``cache_batch_idx``,
+    ``cache_leftpad`` and ``softcap`` raise PkvError(PKV_EUNSUPPORTED).
     """
-    if rotary_cos is not None or rotary_sin is not None:
-        raise PkvError(PKV_EUNSUPPORTED, "rotary embedding of the new K")
     if cache_batch_idx is not None or cache_leftpad is not None:
         raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
     if softcap:
@@ -461,7 +489,10 @@ def flash_attn_with_kvcache(
         lse = torch.empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32, device=q.device)
     out = decode(q.contiguous(), k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, k_new=k,
                  v_new=v, causal=causal, window_size=window_size,
-                 alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous(), softmax_lse=lse)
+                 alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous(), softmax_lse=lse,
+                 rotary_cos=None if rotary_cos is None else rotary_cos.contiguous(),
+                 rotary_sin=None if rotary_sin is None else rotary_sin.contiguous(),
+                 rotary_interleaved=rotary_interleaved)
     return (out, lse) if return_softmax_lse else out
 
 

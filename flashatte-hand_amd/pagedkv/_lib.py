@@ -88,6 +88,11 @@ class PkvDecodeDesc(ctypes.Structure):
         ("k_scale", ctypes.c_void_p),
         ("v_scale", ctypes.c_void_p),
         ("softmax_lse", ctypes.c_void_p),
+        ("rotary_cos", ctypes.c_void_p),
+        ("rotary_sin", ctypes.c_void_p),
+        ("rotary_seqlen", ctypes.c_int64),
+        ("rotary_dim", ctypes.c_int32),
+        ("rotary_interleaved", ctypes.c_int32),
     ]
 
 

@@ -109,6 +109,21 @@ typedef struct pkv_decode_desc {
                                    log(sum_j exp(softmax_scale * q . k_j + bias_j)) over the keys each
                                    query row attends, natural log; +inf for a row with no visible key
                                    (flash-attn 2.6.3's convention).  NULL = not written. */
+    /* Rotary embedding of the appended keys and of q (flash-attn's rotary_cos /
+     * rotary_sin / rotary_interleaved; pkv_decode_append only, which then needs
+     * seqlen_new >= 1).  New token j of row b is rotated at position
+     * max(cache_seqlens[b], 0) + j before it is stored; q token i at that
+     * position + i for a causal or windowed call, else at max(cache_seqlens[b], 0)
+     * (flash-attn 2.6.3).  Pair (x0, x1) with angle index a becomes
+     * (x0 cos[pos][a] - x1 sin[pos][a], x0 sin[pos][a] + x1 cos[pos][a]) in fp32
+     * (no fused multiply-add), rounded to the dtype; interleaved pairs are dims
+     * (2a, 2a + 1), otherwise (a, a + rotary_dim / 2) (GPT-NeoX); dims from
+     * rotary_dim on are unchanged.  V is not rotated. */
+    const void* rotary_cos;     /* [rotary_seqlen, rotary_dim / 2], the dtype of q; NULL = no rotary */
+    const void* rotary_sin;     /* the same shape and dtype */
+    int64_t rotary_seqlen;      /* rows of the tables; at least block_table_stride * page_size */
+    int32_t rotary_dim;         /* multiple of 16, at most head_dim */
+    int32_t rotary_interleaved; /* 1: pairs (2a, 2a + 1); 0: (a, a + rotary_dim / 2) */
 } pkv_decode_desc;
 
 /*

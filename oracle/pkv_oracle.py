@@ -286,6 +286,50 @@ def appended_seqlens(seqlens, seqlen_new):
     return (np.maximum(np.asarray(seqlens, dtype=np.int64), 0) + seqlen_new).astype(np.int32)
 
 
+# ------------------------------------------------------------------ rotary embedding (numpy)
+#
+# flash-attn 2.6.3 flash_attn_with_kvcache(rotary_cos=, rotary_sin=,
+# rotary_interleaved=) (the reference's evaluator passes rotary_interleaved=False
+# and no tables, scripts/evaluate_flashattn_submission.py:244): with new keys
+# k / v, key j of row b is rotated at position cache_seqlens[b] + j; query i at
+# cache_seqlens[b] + i when the call is causal or local, else at
+# cache_seqlens[b].  Pair (x0, x1) of angle index a becomes
+# (x0 cos_a - x1 sin_a, x0 sin_a + x1 cos_a); interleaved pairs are dims
+# (2a, 2a + 1), otherwise (a, a + rotary_dim / 2).  Here every product and sum
+# is one float32 operation (numpy rounds each), and the result is rounded to
+# the 16-bit dtype.
+
+def rotary(x_bits, cos_bits, sin_bits, positions, rotary_dim, interleaved, dtype):
+    """x_bits [..., D] (16-bit patterns) rotated at integer positions [...] (broadcast over the
+    leading dims; clipped to the tables' rows); returns 16-bit patterns of the same shape."""
+    x = bits_to_f32(x_bits, dtype)
+    cos = bits_to_f32(cos_bits, dtype)
+    sin = bits_to_f32(sin_bits, dtype)
+    pos = np.clip(np.asarray(positions, dtype=np.int64), 0, cos.shape[0] - 1)
+    c = cos[pos]  # [..., rotary_dim / 2]
+    s = sin[pos]
+    half = rotary_dim // 2
+    if interleaved:
+        i0 = np.arange(0, rotary_dim, 2)
+        i1 = i0 + 1
+    else:
+        i0 = np.arange(half)
+        i1 = i0 + half
+    x0 = x[..., i0]
+    x1 = x[..., i1]
+    y = x.copy()
+    y[..., i0] = x0 * c - x1 * s
+    y[..., i1] = x0 * s + x1 * c
+    return f32_to_bits(y, dtype)
+
+
+def rotary_positions(seqlens, n, shift):
+    """Positions [B, n] of tokens 0 .. n-1 of each row: max(seqlens, 0) + j when shift, else
+    max(seqlens, 0) for every token (flash-attn's query positions without a causal or local mask)."""
+    base = np.maximum(np.asarray(seqlens, dtype=np.int64), 0)[:, None]
+    return base + (np.arange(n, dtype=np.int64)[None, :] if shift else np.zeros((1, n), dtype=np.int64))
+
+
 
 # ------------------------------------------------------------------ OCP FP8 e4m3 (numpy)
 #

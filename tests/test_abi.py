@@ -408,3 +408,63 @@ def test_left_window_shrinks_the_tile_schedule():
     # C2 with a 1024-token window: 25.5 µs single pass against 28.7 µs tile schedule on MI355X.
     c2w = base_desc(max_seqlen=4096, window_size=(1024, -1))
     assert pagedkv.schedule_for(c2w, 0) == pagedkv.PKV_SCHED_SINGLE
+
+
+# ------------------------------------------------------------------ softmax_lse, rotary tables
+
+def test_misaligned_softmax_lse_is_rejected():
+    d = base_desc(softmax_lse=4098)
+    assert pagedkv.workspace_size(d, 0) == 0
+    assert pagedkv.workspace_size(base_desc(softmax_lse=4096), 0) == pagedkv.workspace_size(base_desc(), 0)
+
+
+def rotary_desc(**kw):
+    r = dict(rotary_cos=8192, rotary_sin=16384, rotary_seqlen=64 * 64, rotary_dim=128, rotary_interleaved=False)
+    r.update(kw)
+    return base_desc(**r)
+
+
+@pytest.mark.parametrize("field,value", [
+    ("rotary_sin", 0),            # tables come in pairs
+    ("rotary_dim", 0),
+    ("rotary_dim", 40),           # not a multiple of 16
+    ("rotary_dim", 256),          # past head_dim
+    ("rotary_seqlen", 64 * 64 - 1),  # fewer rows than a block-table row addresses
+    ("rotary_cos", 8193),         # misaligned
+    ("rotary_interleaved", 2),
+])
+def test_invalid_rotary_tables_are_rejected(field, value):
+    lib = _lib.load()
+    d = rotary_desc(**{field: value})
+    if field == "rotary_interleaved":
+        d.rotary_interleaved = value
+    assert lib.pkv_decode_append_workspace_size(ctypes.byref(d), 0, 1) == 0
+    p = ctypes.c_void_p(4096)
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, 1, 0.1, 0, p, ctypes.byref(d), None) == pagedkv.PKV_EINVAL
+
+
+def test_rotary_tables_belong_to_decode_append_only():
+    """flash-attn 2.6.3 asks for new keys with rotary tables: the entry points without them,
+    and a decode_append of zero new tokens, refuse before launching anything."""
+    lib = _lib.load()
+    d = rotary_desc()
+    p = ctypes.c_void_p(4096)
+    E = pagedkv.PKV_EINVAL
+    assert lib.pkv_decode(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None) == E
+    assert lib.pkv_decode_noalloc(p, p, p, p, p, 0.1, 0, p, ctypes.byref(d), None) == E
+    assert lib.pkv_append_kv(p, p, p, p, p, p, 1, ctypes.byref(d), None) == E
+    assert lib.pkv_reshape_and_cache(p, p, p, p, p, 4, ctypes.byref(d), None) == E
+    assert lib.pkv_decode_append(p, p, p, p, p, p, p, 0, 0.1, 0, p, ctypes.byref(d), None) == E
+
+
+def test_rotary_workspace_adds_the_rotated_queries_and_never_folds():
+    lib = _lib.load()
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for M in (1, 4):
+        plain = base_desc(seqlen_q=M)
+        rot = rotary_desc(seqlen_q=M)
+        extra = align(32 * M * 32 * 128 * 2)
+        assert lib.pkv_decode_append_workspace_size(ctypes.byref(rot), 0, M) == \
+            lib.pkv_decode_append_workspace_size(ctypes.byref(plain), 0, M) + extra
+    assert lib.pkv_decode_append_folds(ctypes.byref(base_desc()), 0, 1) == 1
+    assert lib.pkv_decode_append_folds(ctypes.byref(rotary_desc()), 0, 1) == 0
