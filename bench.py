@@ -146,6 +146,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         seqlen_q=M, causal=args.causal, window_size=tuple(args.window),
         kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
         k_scale=base["k_scale"].data_ptr() if fp8 else 0, v_scale=base["v_scale"].data_ptr() if fp8 else 0,
+        softcap=args.softcap,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
@@ -457,6 +458,8 @@ def main() -> int:
     ap.add_argument("--causal", action="store_true", help="causal mask (decode op, with --seqlen-q > 1)")
     ap.add_argument("--window", type=int, nargs=2, default=(-1, -1), metavar=("LEFT", "RIGHT"),
                     help="sliding window (decode op); -1 = unbounded")
+    ap.add_argument("--softcap", type=float, default=0.0,
+                    help="score softcap (decode op): softcap * tanh(s / softcap), flash-attn's softcap")
     ap.add_argument("--kv", choices=("same", "fp8"), default="same",
                     help="KV cache element type (decode op): the config's 16-bit dtype, or OCP FP8 e4m3 with "
                          "per-KV-head scales")
@@ -516,7 +519,8 @@ def main() -> int:
                        "path": res["path"], "kv_sets": args.sets,
                        **({"seqlen_q": args.seqlen_q, "causal": args.causal} if args.seqlen_q > 1 else {}),
                        **({"window": list(args.window)} if tuple(args.window) != (-1, -1) else {}),
-                       **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {})},
+                       **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {}),
+                       **({"softcap": args.softcap} if args.softcap > 0 else {})},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
             "us_spread": res["spread"],
@@ -528,7 +532,8 @@ def main() -> int:
             "cpu_baseline": None,
         }
         # The CPU baseline restates the reference's own path: 16-bit caches, one query token.
-        if name == args.config and not args.no_cpu and args.kv == "same" and args.seqlen_q == 1:
+        if name == args.config and not args.no_cpu and args.kv == "same" and args.seqlen_q == 1 and \
+                args.softcap == 0:
             line["cpu_baseline"] = cpu_baseline(res, torch, args.cpu_budget)
         res.pop("host_arrays", None)
         lines.append(line)

@@ -114,7 +114,8 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if ((d->mask & PKV_MASK_WINDOW) != 0 && (d->window_left < -1 || d->window_right < -1)) {
         return PKV_EINVAL;
     }
-    if ((reinterpret_cast<uintptr_t>(d->softmax_lse) & 3u) != 0) {
+    if ((reinterpret_cast<uintptr_t>(d->softmax_lse) & 3u) != 0 || !(d->softcap >= 0.f) ||
+        !std::isfinite(d->softcap)) {
         return PKV_EINVAL;
     }
     // Rotary tables: both or neither; rotary_dim a multiple of 16 within the
@@ -165,7 +166,7 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (M == 1) {
         r.win_right = -1;
     }
-    r.multi_query = M > 1 || r.win_left >= 0 || r.win_right >= 0 || d->alibi_slopes != nullptr;
+    r.multi_query = M > 1 || r.win_left >= 0 || r.win_right >= 0 || d->alibi_slopes != nullptr || d->softcap > 0.f;
     r.page_shift = ilog2(r.P);
     const int64_t row_cap = d->block_table_stride * r.P;
     const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
@@ -514,6 +515,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.k_scale = desc->k_scale;
     p.v_scale = desc->v_scale;
     p.lse = desc->softmax_lse;
+    p.softcap_log2 = desc->softcap * 1.4426950408889634074f;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);

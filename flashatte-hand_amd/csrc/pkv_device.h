@@ -60,6 +60,7 @@ struct PartitionParams {
     const float* k_scale;
     const float* v_scale;
     float* lse;           // optional fp32 [B, H, M]: natural-log LSE of each output row (store_lse)
+    float softcap_log2;   // > 0: every score x (log2 units) becomes softcap_log2 * tanh(x / softcap_log2)
 };
 
 struct CombineParams {
@@ -244,6 +245,13 @@ __device__ __forceinline__ uint4 load_kv16(const uint16_t* ptr) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// tanh x = sign(x) (1 - e) / (1 + e) with e = exp(-2 |x|) from the hardware
+// exp2 and reciprocal (about 2 ulp relative, 1e-7 absolute near 0).
+__device__ __forceinline__ float tanh_f32(float x) {
+    const float e = fast_exp2(-2.8853900817779268f * fabsf(x));
+    return copysignf((1.f - e) * __builtin_amdgcn_rcpf(1.f + e), x);
+}
 
 // flash-attn's softmax_lse ([B, H, M], natural log) of output row `row` of
 // [B, M, H]: (m2 + log2 l) * ln 2 from a log2-domain max m2 and the weight sum

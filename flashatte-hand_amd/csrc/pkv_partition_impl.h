@@ -306,6 +306,8 @@ struct MfmaMath {
         int32_t all_lo; // max over the slice's rows of lo
         int32_t all_hi; // min over the slice's rows of hi
         bool alibi;
+        float cap;      // softcap in log2 units (0 = none) and its reciprocal
+        float inv_cap;
     };
     // Per block: O^T tiles (lane (n, j): row n, dims 16 dt + 4j .. +3),
     // reference max, denominator.
@@ -391,6 +393,8 @@ struct MfmaMath {
             q.all_lo = uniform(all_lo);
             q.all_hi = uniform(all_hi);
             q.alibi = p.alibi != nullptr;
+            q.cap = p.softcap_log2;
+            q.inv_cap = p.softcap_log2 > 0.f ? 1.f / p.softcap_log2 : 0.f;
         }
     }
 
@@ -428,11 +432,15 @@ struct MfmaMath {
             }
         }
         // Lane holds row 16 nb + n, tokens 4j + i.  MQ: tiles every row sees
-        // whole, without ALiBi, take the plain path (a wave-uniform test).
+        // whole, without ALiBi or a softcap, take the plain path (a
+        // wave-uniform test).  The softcap (flash-attn's) applies to the
+        // scaled score before the ALiBi bias.
         float sc[NB][4];
         bool plain = true;
+        bool capped = false;
         if constexpr (MQ) {
-            plain = !q.alibi && t0 >= q.all_lo && t0 + 16 <= q.all_hi && t0 + 16 <= end;
+            capped = q.cap > 0.f;
+            plain = !q.alibi && !capped && t0 >= q.all_lo && t0 + 16 <= q.all_hi && t0 + 16 <= end;
         }
         if (plain) {
 #pragma unroll
@@ -448,7 +456,11 @@ struct MfmaMath {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = t0 + 4 * j + i;
-                    const float x = s[nb][i] * scale_log2 - q.slope[nb] * fabsf(static_cast<float>(q.pos[nb] - t));
+                    float x = s[nb][i] * scale_log2;
+                    if (capped) {
+                        x = q.cap * tanh_f32(x * q.inv_cap);
+                    }
+                    x -= q.slope[nb] * fabsf(static_cast<float>(q.pos[nb] - t));
                     sc[nb][i] = (t < end && t >= q.lo[nb] && t < q.hi[nb]) ? x : kNegInf;
                 }
             }
@@ -1351,7 +1363,8 @@ static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, cons
 template <bool BF16, int D>
 static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wave, hipStream_t stream,
                            const LaunchEvents& ev) {
-    const bool multi_query = p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr;
+    const bool multi_query =
+        p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr || p.softcap_log2 > 0.f;
     if (mfma) {
         // 16 or 32 query rows per wave (heads_per_wave).
         if (heads_per_wave == 32) {

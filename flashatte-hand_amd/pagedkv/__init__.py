@@ -111,6 +111,7 @@ def make_desc(
     rotary_seqlen: int = 0,
     rotary_dim: int = 0,
     rotary_interleaved: bool = True,
+    softcap: float = 0.0,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -143,6 +144,7 @@ def make_desc(
     d.rotary_seqlen = rotary_seqlen
     d.rotary_dim = rotary_dim
     d.rotary_interleaved = 1 if rotary_interleaved else 0
+    d.softcap = softcap
     return d
 
 
@@ -226,8 +228,12 @@ def decode(
     rotary_cos=None,
     rotary_sin=None,
     rotary_interleaved: bool = True,
+    softcap: float = 0.0,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
+
+    ``softcap`` > 0 caps each scaled score s to softcap * tanh(s / softcap)
+    before the ALiBi bias (flash-attn's softcap).
 
     ``rotary_cos`` / ``rotary_sin`` ([seqlen_ro, rotary_dim / 2], q's dtype;
     with ``k_new``) rotate the new keys at their positions before they are
@@ -314,7 +320,7 @@ def decode(
         split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
         alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride, kv_dtype=kv_dtype,
         k_scale=_scale_ptr("k_scale", k_scale, Hk), v_scale=_scale_ptr("v_scale", v_scale, Hk),
-        softmax_lse=lse_ptr, **rot,
+        softmax_lse=lse_ptr, softcap=float(softcap), **rot,
     )
     lib = _lib.load()
     if seqlen_new:
@@ -467,13 +473,12 @@ def flash_attn_with_kvcache(
     ``return_softmax_lse`` returns ``(out, softmax_lse)`` with softmax_lse fp32
     ``[B, H, M]`` (natural log, +inf for a row with no visible key);
     ``rotary_cos`` / ``rotary_sin`` with ``k`` / ``v`` rotate the new keys and
-    q (``rotary_interleaved`` as in flash-attn).  ``cache_batch_idx``,
-    ``cache_leftpad`` and ``softcap`` raise PkvError(PKV_EUNSUPPORTED).
+    q (``rotary_interleaved`` as in flash-attn); ``softcap`` > 0 caps the
+    scores.  ``cache_batch_idx`` and ``cache_leftpad`` raise
+    PkvError(PKV_EUNSUPPORTED).
     """
     if cache_batch_idx is not None or cache_leftpad is not None:
         raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
-    if softcap:
-        raise PkvError(PKV_EUNSUPPORTED, "softcap")
     if block_table is None or cache_seqlens is None:
         raise PkvError(PKV_EUNSUPPORTED, "only the paged layout (block_table + cache_seqlens) is implemented")
     if isinstance(cache_seqlens, int):
@@ -492,7 +497,7 @@ def flash_attn_with_kvcache(
                  alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous(), softmax_lse=lse,
                  rotary_cos=None if rotary_cos is None else rotary_cos.contiguous(),
                  rotary_sin=None if rotary_sin is None else rotary_sin.contiguous(),
-                 rotary_interleaved=rotary_interleaved)
+                 rotary_interleaved=rotary_interleaved, softcap=softcap)
     return (out, lse) if return_softmax_lse else out
 
 

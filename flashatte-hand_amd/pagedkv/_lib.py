@@ -93,6 +93,7 @@ class PkvDecodeDesc(ctypes.Structure):
         ("rotary_seqlen", ctypes.c_int64),
         ("rotary_dim", ctypes.c_int32),
         ("rotary_interleaved", ctypes.c_int32),
+        ("softcap", ctypes.c_float),
     ]
 
 

@@ -124,6 +124,9 @@ typedef struct pkv_decode_desc {
     int64_t rotary_seqlen;      /* rows of the tables; at least block_table_stride * page_size */
     int32_t rotary_dim;         /* multiple of 16, at most head_dim */
     int32_t rotary_interleaved; /* 1: pairs (2a, 2a + 1); 0: (a, a + rotary_dim / 2) */
+    float softcap;              /* > 0: each scaled score s becomes softcap * tanh(s / softcap) before the
+                                   ALiBi bias (flash-attn's softcap, as in Gemma 2); 0 = off.  Needs the
+                                   MFMA path. */
 } pkv_decode_desc;
 
 /*

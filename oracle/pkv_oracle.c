@@ -390,7 +390,7 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
                           const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_q, int causal,
                           int64_t window_left, int64_t window_right, const float* alibi_slopes,
                           int64_t alibi_batch_stride, int kv_fp8, const float* k_scale, const float* v_scale,
-                          double softmax_scale, double* out, double* lse) {
+                          double softmax_scale, double* out, double* lse, double softcap) {
     build_f16_table();
     set_threads(d);
     const int64_t B = d->batch, H = d->num_heads, D = d->head_dim, M = seqlen_q;
@@ -453,7 +453,11 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
                 for (int64_t c = 0; c < D; ++c) {
                     s += qd[c] * kv_elem(k_cache, koff + c, dt, kv_fp8, ks);
                 }
-                scores[t] = s * softmax_scale - slope * fabs((double)(pos - t));
+                double x = s * softmax_scale;
+                if (softcap > 0.0) {
+                    x = softcap * tanh(x / softcap);
+                }
+                scores[t] = x - slope * fabs((double)(pos - t));
                 if (scores[t] > mx) {
                     mx = scores[t];
                 }
@@ -489,18 +493,19 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                          const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out, double* lse) {
+                         double* out, double* lse, double softcap) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out, lse);
+                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out, lse, softcap);
 }
 
 void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint8_t* k_cache,
                           const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                           int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                           const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
-                          const float* v_scale, double softmax_scale, double* out, double* lse) {
+                          const float* v_scale, double softmax_scale, double* out, double* lse,
+                          double softcap) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out, lse);
+                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out, lse, softcap);
 }
 
 /* ---------------------------------------------------------------- split-KV algebra */

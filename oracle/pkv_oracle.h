@@ -62,12 +62,14 @@ void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const ui
  * -slope * |pos - t| to the scaled score.  A query without a visible key
  * gives zeros.  out is fp64.  lse (optional, fp64 [B, H, seqlen_q]): each
  * query's log(sum over its visible keys of exp(score)), natural log, +inf for
- * a query without a visible key (flash-attn's softmax_lse). */
+ * a query without a visible key (flash-attn's softmax_lse).  softcap > 0:
+ * each scaled score s becomes softcap * tanh(s / softcap) before the ALiBi
+ * term (flash-attn 2.6.3's softcap). */
 void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
                          const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out, double* lse);
+                         double* out, double* lse, double softcap);
 
 /* OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 = NaN, max 448) to fp32. */
 float pkv_oracle_e4m3_to_f32(uint8_t b);
@@ -78,7 +80,7 @@ void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uin
                           const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                           int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                           const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
-                          const float* v_scale, double softmax_scale, double* out, double* lse);
+                          const float* v_scale, double softmax_scale, double* out, double* lse, double softcap);
 
 /* Split-KV partition step (best_flashattn_kvcache_decode.cu:664-697, 782-864):
  * split s of row b covers pages [n*s/S, n*(s+1)/S) of its n valid pages;

@@ -70,12 +70,13 @@ def load():
     lib.pkv_oracle_combine_f32.restype = None
     lib.pkv_oracle_attn_f64.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
-                                        ctypes.c_double, _f64p, ctypes.c_void_p]
+                                        ctypes.c_double, _f64p, ctypes.c_void_p, ctypes.c_double]
     lib.pkv_oracle_attn_f64.restype = None
     _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
     lib.pkv_oracle_attn8_f64.argtypes = [dp, _u16p, _u8p, _u8p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
                                          ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
-                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double, _f64p, ctypes.c_void_p]
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double, _f64p, ctypes.c_void_p,
+                                         ctypes.c_double]
     lib.pkv_oracle_attn8_f64.restype = None
     lib.pkv_oracle_e4m3_to_f32.argtypes = [ctypes.c_uint8]
     lib.pkv_oracle_e4m3_to_f32.restype = ctypes.c_float
@@ -129,10 +130,10 @@ def decode_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, threads=
 
 
 def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=False, window=(-1, -1),
-             alibi=None, threads=0, lse=False):
+             alibi=None, threads=0, lse=False, softcap=0.0):
     """Dense fp64 attention of q [B, M, H, D] with flash-attn 2.6.3 masks; returns float64 [B, M, H, D],
     and with lse=True also the float64 softmax_lse [B, H, M] (natural log, +inf for a query without a
-    visible key).
+    visible key).  softcap > 0 caps each scaled score s to softcap * tanh(s / softcap) before ALiBi.
 
     alibi: None, fp32 [H] or [B, H] slopes."""
     lib = load()
@@ -150,12 +151,13 @@ def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=Fal
                             _c(block_table, np.int32), _c(seqlens, np.int32), int(M), int(bool(causal)),
                             int(window[0]), int(window[1]),
                             None if slopes is None else slopes.ctypes.data_as(ctypes.c_void_p), int(stride),
-                            float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p))
+                            float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p),
+                            float(softcap))
     return (out, lse_out) if lse else out
 
 
 def attn8_f64(q, k_cache8, v_cache8, block_table, seqlens, scale, dtype, k_scale=None, v_scale=None, causal=False,
-              window=(-1, -1), alibi=None, threads=0, lse=False):
+              window=(-1, -1), alibi=None, threads=0, lse=False, softcap=0.0):
     """attn_f64 over OCP FP8 e4m3 caches (uint8 [num_pages, P, Hk, D]) with per-KV-head fp32 scales."""
     lib = load()
     B, M, H, D = q.shape
@@ -178,7 +180,8 @@ def attn8_f64(q, k_cache8, v_cache8, block_table, seqlens, scale, dtype, k_scale
     lib.pkv_oracle_attn8_f64(ctypes.byref(d), _c(q, np.uint16), _c(k_cache8, np.uint8), _c(v_cache8, np.uint8),
                              _c(block_table, np.int32), _c(seqlens, np.int32), int(M), int(bool(causal)),
                              int(window[0]), int(window[1]), ptr(alibi), int(stride), ptr(k_scale), ptr(v_scale),
-                             float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p))
+                             float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p),
+                             float(softcap))
     return (out, lse_out) if lse else out
 
 

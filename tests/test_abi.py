@@ -468,3 +468,15 @@ def test_rotary_workspace_adds_the_rotated_queries_and_never_folds():
             lib.pkv_decode_append_workspace_size(ctypes.byref(plain), 0, M) + extra
     assert lib.pkv_decode_append_folds(ctypes.byref(base_desc()), 0, 1) == 1
     assert lib.pkv_decode_append_folds(ctypes.byref(rotary_desc()), 0, 1) == 0
+
+
+@pytest.mark.parametrize("value", [-1.0, float("nan"), float("inf")])
+def test_invalid_softcap_is_rejected(value):
+    assert pagedkv.workspace_size(base_desc(softcap=value), 0) == 0
+
+
+def test_softcap_needs_the_mfma_path_and_takes_the_masked_policy():
+    assert pagedkv.workspace_size(base_desc(softcap=30.0), 0) > 0
+    assert pagedkv.workspace_size(base_desc(softcap=30.0, path=pagedkv.PKV_PATH_VALU), 0) == 0
+    lib = _lib.load()
+    assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(softcap=30.0)), 0, 1) == 0

@@ -311,7 +311,7 @@ def test_flash_attn_api_and_explicit_stream(rng):
     s.synchronize()
     assert (from_dev(out) == ref).all()
     with pytest.raises(pagedkv.PkvError):
-        pagedkv.flash_attn_with_kvcache(*args, cache_seqlens=sld, block_table=btd, softcap=30.0)
+        pagedkv.flash_attn_with_kvcache(*args, cache_seqlens=sld, block_table=btd, cache_leftpad=sld)
 
 
 # ------------------------------------------------------------------ the five BASELINE configs at full size
