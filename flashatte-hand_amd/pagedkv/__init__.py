@@ -441,6 +441,35 @@ def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *,
         raise PkvError(st, "pkv_reshape_and_cache")
 
 
+def _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx):
+    """flash-attn's contiguous caches [B_cache, S, Hk, D] as a paged pool: pages of P tokens
+    (the largest power of two up to 1024 dividing S), row b of the batch on the pages of cache
+    row cache_batch_idx[b] (or b).  Returns the paged views and the block table."""
+    torch = _torch()
+    for name, t in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_cuda(name, t)
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise PkvError(PKV_EINVAL, "k_cache / v_cache must both be [B_cache, seqlen_cache, Hk, D]")
+    b_cache, S, Hk, D = k_cache.shape
+    B = q.shape[0]
+    if S < 1:
+        raise PkvError(PKV_EINVAL, "empty cache")
+    P = min(S & -S, 1024)
+    per_row = S // P
+    if cache_batch_idx is None:
+        if b_cache < B:
+            raise PkvError(PKV_EINVAL, "k_cache has fewer rows than the batch")
+        rows = torch.arange(B, dtype=torch.int64, device=q.device)
+    else:
+        _check_cuda("cache_batch_idx", cache_batch_idx)
+        if cache_batch_idx.dim() != 1 or cache_batch_idx.shape[0] != B:
+            raise PkvError(PKV_EINVAL, "cache_batch_idx must be [B]")
+        rows = cache_batch_idx.to(torch.int64)
+    table = rows[:, None] * per_row + torch.arange(per_row, dtype=torch.int64, device=q.device)[None, :]
+    return (k_cache.view(b_cache * per_row, P, Hk, D), v_cache.view(b_cache * per_row, P, Hk, D),
+            table.to(torch.int32).contiguous())
+
+
 def flash_attn_with_kvcache(
     q,
     k_cache,
@@ -474,15 +503,29 @@ def flash_attn_with_kvcache(
     ``[B, H, M]`` (natural log, +inf for a row with no visible key);
     ``rotary_cos`` / ``rotary_sin`` with ``k`` / ``v`` rotate the new keys and
     q (``rotary_interleaved`` as in flash-attn); ``softcap`` > 0 caps the
-    scores.  ``cache_batch_idx`` and ``cache_leftpad`` raise
-    PkvError(PKV_EUNSUPPORTED).
+    scores.
+
+    Without ``block_table`` the caches are flash-attn's contiguous ones,
+    ``[B_cache, seqlen_cache, Hk, D]``, row b of the batch reading cache row
+    ``cache_batch_idx[b]`` (b without it); ``cache_seqlens`` None means every
+    row holds seqlen_cache tokens.  They are attended as pages of the largest
+    power of two up to 1024 that divides seqlen_cache, through a block table
+    built here (one small device tensor).  ``cache_leftpad`` raises
+    PkvError(PKV_EUNSUPPORTED), and so does ``cache_batch_idx`` with a block
+    table (flash-attn 2.6.3 refuses both with paged caches too).
     """
-    if cache_batch_idx is not None or cache_leftpad is not None:
-        raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx / cache_leftpad")
-    if block_table is None or cache_seqlens is None:
-        raise PkvError(PKV_EUNSUPPORTED, "only the paged layout (block_table + cache_seqlens) is implemented")
+    torch = _torch()
+    if cache_leftpad is not None:
+        raise PkvError(PKV_EUNSUPPORTED, "cache_leftpad")
+    if block_table is None:
+        k_cache, v_cache, block_table = _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx)
+        if cache_seqlens is None:
+            cache_seqlens = int(block_table.shape[1] * k_cache.shape[1])
+    elif cache_batch_idx is not None:
+        raise PkvError(PKV_EUNSUPPORTED, "cache_batch_idx with a block table")
+    if cache_seqlens is None:
+        raise PkvError(PKV_EINVAL, "cache_seqlens is needed with a block table")
     if isinstance(cache_seqlens, int):
-        torch = _torch()
         cache_seqlens = torch.full((q.shape[0],), cache_seqlens, dtype=torch.int32, device=q.device)
     if k is not None:
         k = k.contiguous()
