@@ -324,36 +324,52 @@ def run_append(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
 
 
 def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
-    """Decode step with one new token per row appended in the call; rows end at the config's lengths."""
+    """Decode step with M = --seqlen-q new tokens per row appended in the call (one by default;
+    M > 1 with --causal is the speculative verify step); rows end at the config's lengths."""
     from pagedkv.configs import make_config, make_tensors
 
     cfg = make_config(name)
+    M = max(1, args.seqlen_q)
+    fp8 = args.kv == "fp8"
     sets = [make_tensors(cfg, "cuda", seed=cfg.seed + 7919 * i) for i in range(max(1, args.sets))]
     dev = torch.device("cuda")
+    new_dtype = sets[0]["k_cache"].dtype
+    for s_ in sets:
+        if fp8:
+            for key in ("k_cache", "v_cache"):
+                s_[key] = s_[key].float().clamp(-448, 448).to(torch.float8_e4m3fn)
+            s_["k_scale"] = torch.rand(cfg.num_heads_k, device=dev) + 0.5
+            s_["v_scale"] = torch.rand(cfg.num_heads_k, device=dev) + 0.5
+        if M > 1:
+            s_["q"] = torch.randn((cfg.batch, M, cfg.num_heads, cfg.head_dim), device=dev).to(s_["q"].dtype)
     sh = torch.cuda.current_stream(dev).cuda_stream
     base = sets[0]
     desc = pagedkv.make_desc(
         batch=cfg.batch, num_heads=cfg.num_heads, num_heads_k=cfg.num_heads_k, head_dim=cfg.head_dim,
         page_size=cfg.page_size, num_pages=base["k_cache"].shape[0], block_table_stride=cfg.block_table.shape[1],
         dtype=pagedkv.PKV_DTYPE_F16 if cfg.dtype == "f16" else pagedkv.PKV_DTYPE_BF16,
-        max_seqlen=int(cfg.seqlens.max()) - 1, path=args.path,
+        max_seqlen=int(cfg.seqlens.max()) - M, path=args.path, seqlen_q=M, causal=args.causal,
+        kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
+        k_scale=base["k_scale"].data_ptr() if fp8 else 0, v_scale=base["v_scale"].data_ptr() if fp8 else 0,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     lib = pagedkv._lib.load()
-    ws_bytes = lib.pkv_decode_append_workspace_size(ctypes.byref(desc), splits_req, 1)
+    ws_bytes = lib.pkv_decode_append_workspace_size(ctypes.byref(desc), splits_req, M)
     ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
     desc.workspace = ws.data_ptr()
     desc.workspace_bytes = ws_bytes
-    prev = [(s["cache_seqlens"] - 1).clamp(min=0).to(torch.int32).contiguous() for s in sets]
-    shape = (cfg.batch, 1, cfg.num_heads_k, cfg.head_dim)
-    news = [(torch.randn(shape, device=dev).to(base["k_cache"].dtype),
-             torch.randn(shape, device=dev).to(base["k_cache"].dtype)) for _ in sets]
+    prev = [(s["cache_seqlens"] - M).clamp(min=0).to(torch.int32).contiguous() for s in sets]
+    shape = (cfg.batch, M, cfg.num_heads_k, cfg.head_dim)
+    news = [(torch.randn(shape, device=dev).to(new_dtype), torch.randn(shape, device=dev).to(new_dtype))
+            for _ in sets]
     outs = [torch.empty_like(s["q"]) for s in sets]
 
     def call(i):
         s, (kn, vn), sl, o = sets[i % len(sets)], news[i % len(sets)], prev[i % len(sets)], outs[i % len(sets)]
+        if fp8:
+            desc.k_scale, desc.v_scale = s["k_scale"].data_ptr(), s["v_scale"].data_ptr()
         st = lib.pkv_decode_append(s["q"].data_ptr(), kn.data_ptr(), vn.data_ptr(), s["k_cache"].data_ptr(),
-                                   s["v_cache"].data_ptr(), s["block_table"].data_ptr(), sl.data_ptr(), 1,
+                                   s["v_cache"].data_ptr(), s["block_table"].data_ptr(), sl.data_ptr(), M,
                                    float(cfg.scale), splits_req, o.data_ptr(), ctypes.byref(desc), sh)
         if st != 0:
             raise pagedkv.PkvError(st, "pkv_decode_append")
@@ -369,7 +385,9 @@ def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dic
     torch.cuda.synchronize()
     ms = events.elapsed_ms(t_start, t_end) / args.steps
     events.destroy([t_start, t_end])
-    return {"cfg": cfg, "ms": ms, "kv_gbps": cfg.kv_bytes() / (ms * 1e-3) / 1e9}
+    kv_bytes = cfg.kv_bytes() // 2 if fp8 else cfg.kv_bytes()
+    return {"cfg": cfg, "ms": ms, "kv_gbps": kv_bytes / (ms * 1e-3) / 1e9,
+            "folded": bool(lib.pkv_decode_append_folds(ctypes.byref(desc), splits_req, M) == 1)}
 
 
 def cpu_append_baseline(res: dict, torch, budget_s: float) -> dict:
@@ -578,11 +596,16 @@ def run_op(args, torch, pagedkv, events: HipEvents) -> int:
     else:
         res = run_decode_append(args.config, args, torch, pagedkv, events)
         cfg = res["cfg"]
-        line = {"metric": "KV-stream HBM GB/s of a decode step with a one-token append per row",
+        M = max(1, args.seqlen_q)
+        line = {"metric": "KV-stream HBM GB/s of a decode step with its new tokens appended in the call",
                 "value": round(res["kv_gbps"], 1), "unit": "GB/s", **common, "ms_per_step": round(res["ms"], 5),
-                "dtype": cfg.dtype, "config": {**cfg.describe(), "workload": "decode_append", "seqlen_new": 1},
+                "dtype": cfg.dtype,
+                "config": {**cfg.describe(), "workload": "decode_append", "seqlen_new": M, "seqlen_q": M,
+                           "causal": args.causal, "folded": res["folded"],
+                           **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {})},
                 "us_per_call": round(res["ms"] * 1e3, 2), "cpu_baseline": None}
-        print(f"[bench] decode_append {cfg.name}: {res['ms'] * 1e3:.2f} us/call, {res['kv_gbps']:.1f} GB/s KV",
+        print(f"[bench] decode_append {cfg.name} M={M}{' causal' if args.causal else ''} kv={args.kv} "
+              f"folded={res['folded']}: {res['ms'] * 1e3:.2f} us/call, {res['kv_gbps']:.1f} GB/s KV",
               file=sys.stderr, flush=True)
     if args.json_out:
         with open(args.json_out, "a") as f:

@@ -422,7 +422,24 @@ struct AppendFold {
     const void* v_new;
     void* k_cache;
     void* v_cache;
+    bool causal; // query i sees new tokens j <= i (else all of them)
 };
+
+// New tokens a folded append handles per row (kMaxFold in pkv_combine.hip).
+constexpr int64_t kMaxFoldTokens = 8;
+
+// A plan the fold can serve: the tile schedule with its row-per-wave combine,
+// up to kMaxFoldTokens query rows per (b, head), and no window, ALiBi or
+// softcap (the partition runs without masks: every query sits past the cached
+// tokens).
+bool fold_plan_ok(const Resolved& r, const pkv_decode_desc* d, const SplitPlan& plan) {
+    if (plan.schedule != PKV_SCHED_TILES || r.M > kMaxFoldTokens || r.win_left >= 0 || r.win_right >= 0 ||
+        d->alibi_slopes != nullptr || d->softcap > 0.f || r.rotary) {
+        return false;
+    }
+    const CombineForm f = combine_form(r, plan);
+    return !f.by_stream && !f.long_rows && !f.row_groups;
+}
 
 // pkv_decode: validation, then (when `launch`) the partition and combine
 // launches.  With launch == false only the checks run, so a caller that
@@ -454,8 +471,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     if (need > 0 && (desc->workspace == nullptr || desc->workspace_bytes < need || !aligned16(desc->workspace))) {
         return PKV_ENOWORKSPACE;
     }
-    if (fold != nullptr && (!tiles || r.M != 1 || r.multi_query || r.kv_fp8 ||
-                            combine_form(r, plan).by_stream || combine_form(r, plan).long_rows)) {
+    if (fold != nullptr && !fold_plan_ok(r, desc, plan)) {
         return PKV_EUNSUPPORTED;
     }
     const int64_t items = tiles ? 0 : r.B * r.Hk * r.head_groups * splits;
@@ -568,6 +584,10 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
             c.app_bt_stride = p.bt_stride;
             c.app_num_pages = p.num_pages;
             c.app_scale_log2 = p.scale_log2;
+            c.app_causal = fold->causal ? 1 : 0;
+            c.app_kv_fp8 = r.kv_fp8 ? 1 : 0;
+            c.app_k_scale = desc->k_scale;
+            c.app_v_scale = desc->v_scale;
         }
         if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s, comb_ev) != hipSuccess) {
             return PKV_ELAUNCH;
@@ -637,22 +657,27 @@ pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
     return a;
 }
 
-// The one-token append folds into the combine for one query token, 16-bit
-// caches, no window or ALiBi (a causal mask changes nothing for one query
-// token), on the tile schedule with the row-per-wave
-// combine (a few parts per stream): then the partition attends the cached
-// tokens, the combine adds the new one and stores it, and no append kernel
-// runs.  Other calls append first and then attend the longer rows.
-bool fold_fits(const Resolved& r, const pkv_decode_desc* d, int num_splits, int64_t seqlen_new) {
-    if (seqlen_new != 1 || r.multi_query || r.kv_fp8 || r.rotary) {
+// The append folds into the combine when the new tokens are the query tokens
+// (seqlen_new = M <= kMaxFoldTokens, the decode step and the speculative
+// verify step), with no window, ALiBi, softcap or rotary tables, on the tile
+// schedule with the row-per-wave combine (a few parts per stream): the
+// partition attends the cached tokens with `*part` = the appended-length
+// descriptor `a` without its causal mask (every query sits past them), the
+// combine adds the new tokens each query sees and stores them, and no append
+// kernel runs.  Other calls append first and then attend the longer rows.
+bool fold_fits(const pkv_decode_desc* a, int num_splits, int64_t seqlen_new, pkv_decode_desc* part, bool* causal) {
+    Resolved r;
+    if (resolve(a, r) != PKV_OK || seqlen_new != r.M || r.rotary) {
         return false;
     }
-    const SplitPlan plan = resolve_splits(d, r, num_splits);
-    if (plan.schedule != PKV_SCHED_TILES) {
+    *part = *a;
+    *causal = (a->mask & PKV_MASK_CAUSAL) != 0;
+    part->mask &= ~PKV_MASK_CAUSAL;
+    Resolved rp;
+    if (resolve(part, rp) != PKV_OK) {
         return false;
     }
-    const CombineForm f = combine_form(r, plan);
-    return !f.by_stream && !f.long_rows && !f.row_groups;
+    return fold_plan_ok(rp, part, resolve_splits(part, rp, num_splits));
 }
 
 } // namespace
@@ -815,8 +840,13 @@ size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_spl
         return pkv_decode_workspace_size(desc, num_splits);
     }
     const pkv_decode_desc a = appended_desc(desc, seqlen_new);
-    return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + rotary_q_bytes(r) +
-           pkv_decode_workspace_size(&a, num_splits);
+    size_t need = pkv_decode_workspace_size(&a, num_splits);
+    pkv_decode_desc part;
+    bool causal = false;
+    if (fold_fits(&a, num_splits, seqlen_new, &part, &causal)) {
+        need = std::max(need, pkv_decode_workspace_size(&part, num_splits)); // the folded plan's partials
+    }
+    return align_up(static_cast<size_t>(r.B) * sizeof(int32_t)) + rotary_q_bytes(r) + need;
 }
 
 int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new) {
@@ -825,7 +855,9 @@ int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t
         return -1;
     }
     const pkv_decode_desc a = appended_desc(desc, seqlen_new);
-    return fold_fits(r, &a, num_splits, seqlen_new) ? 1 : 0;
+    pkv_decode_desc part;
+    bool causal = false;
+    return fold_fits(&a, num_splits, seqlen_new, &part, &causal) ? 1 : 0;
 }
 
 int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
@@ -858,17 +890,19 @@ int pkv_decode_append(const void* q, const void* k_new, const void* v_new, void*
     pkv_decode_desc a = appended_desc(desc, seqlen_new);
     a.workspace = static_cast<char*>(desc->workspace) + head_bytes;
     a.workspace_bytes = desc->workspace_bytes - head_bytes;
+    // The decode step and the speculative verify step: the partition attends
+    // the cached tokens and the combine adds the new ones and stores them
+    // (two launches instead of three; the lengths region stays unused).
+    pkv_decode_desc part;
+    bool causal = false;
+    if (fold_fits(&a, num_splits, seqlen_new, &part, &causal)) {
+        const AppendFold fold{k_new, v_new, k_cache, v_cache, causal};
+        return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, &part,
+                           stream, true, &fold);
+    }
     if (pkv_decode_workspace_size(&a, num_splits) == 0) {
         a.workspace = nullptr;
         a.workspace_bytes = 0;
-    }
-    // One new token on the common decode shape: the partition attends the
-    // cached tokens and the combine adds the new one and stores it (two
-    // launches instead of three; the lengths region stays unused).
-    if (fold_fits(r, &a, num_splits, seqlen_new)) {
-        const AppendFold fold{k_new, v_new, k_cache, v_cache};
-        return decode_impl(q, k_cache, v_cache, block_table, cache_seqlens, softmax_scale, num_splits, out, &a,
-                           stream, true, &fold);
     }
     // Every check of the attention runs before the cache is written.
     st = decode_impl(q, k_cache, v_cache, block_table, lens, softmax_scale, num_splits, out, &a, stream, false);

@@ -305,6 +305,9 @@ __device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
     return t;
 }
 
+// The decode step's fold on 16-bit caches (one new token, one query token):
+// the general form below with n = 1, written for its registers (the general
+// form needs more and drops the kernel to 3 waves per SIMD at head_dim 256).
 // Row (b, h) of a decode with a one-token append (p.app_k set): the
 // partition attended the row's cache_seqlens[b] cached tokens and left every
 // stream's parts in partial slots (force_partial); the new token j = L (its
@@ -315,7 +318,7 @@ __device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
 // attended (the append kernel skips it too); a page id outside
 // [0, num_pages) is not written, and the token is attended from k_new.
 template <bool BF16, int D, int kBatch>
-__device__ __forceinline__ void combine_append_row(const CombineParams& p, const TileRow& t, int row, int lane,
+__device__ __forceinline__ void combine_append_one(const CombineParams& p, const TileRow& t, int row, int lane,
                                                    uint16_t* dst) {
     constexpr int E = D / 64;
     const int h = row - t.b * p.num_heads;
@@ -394,13 +397,197 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
     }
 }
 
+// Most new tokens a folded append adds per row (query tokens per row then).
+constexpr int kMaxFold = 8;
+
+// Two OCP e4m3 bytes (bytes 0-1, or 2-3 with HI) to two bf16 values, exactly
+// (every e4m3 value is a bf16 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16(uint32_t x) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(x, 1.0f, HI));
+}
+
+// E values of the compute dtype to E OCP e4m3 bytes (packed, lane order):
+// x * inv in fp32, saturated to +-448, rounded to nearest even, as the append
+// kernel stores them; and the bytes' exact values back in fp32.
+template <int E>
+__device__ __forceinline__ uint32_t quantize_e(const float (&x)[E], float inv, float (&back)[E]) {
+    float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float v = x[e] * inv;
+        y[e] = fabsf(v) > 448.f ? copysignf(448.f, v) : v;
+    }
+    uint32_t w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false));
+    w = static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], static_cast<int>(w), true));
+    float a, b;
+    unpack2<true>(fp8x2_to_bf16<false>(w), a, b);
+    back[0] = a;
+    if constexpr (E > 1) {
+        back[1] = b;
+    }
+    if constexpr (E > 2) {
+        unpack2<true>(fp8x2_to_bf16<true>(w), a, b);
+        back[2] = a;
+        back[3] = b;
+    }
+    return w;
+}
+
+// Output row (b, i, h) of a decode whose n = q_len new tokens are folded in
+// (p.app_k set; the speculative-decode form: new token j sits at position
+// L + j, L = max(cache_seqlens[b], 0), and query i at L + i).  The partition
+// attended the row's cached tokens (all of them: every query sits past them)
+// and left every stream's parts in partial slots (force_partial); here the new
+// tokens query i sees (j <= i when causal, all n otherwise) join as parts of
+// weight exp2(s_j - max), s_j the log2-domain score q . k_j, with value v_j.
+// FP8 caches: k_j and v_j are quantised as the append stores them and
+// attended as those bytes' values (times the KV head's scales).  Token j's K
+// and V rows go to slot L + j of the row's block table, written by the wave
+// of query j and the first query head of each KV head.  A position past the
+// block-table row is neither written nor attended (the append kernel skips
+// it too); a page id outside [0, num_pages) is not written, and the token is
+// attended from k_new.
+template <bool BF16, int D, int kBatch, bool FP8, int NF>
+__device__ __forceinline__ void combine_append_row(const CombineParams& p, const TileRow& t, int row, int lane,
+                                                   uint16_t* dst) {
+    constexpr int E = D / 64;
+    const int n = p.q_len;
+    const int per_b = n * p.num_heads;
+    const int i = (row - t.b * per_b) / p.num_heads;
+    const int h = row - t.b * per_b - i * p.num_heads;
+    const int hk = p.num_heads / p.group;
+    const int kvh = h / p.group;
+    const int seen = p.app_causal ? i + 1 : n; // new tokens query i attends
+    // Loads that do not wait on cache_seqlens: q and the new tokens' rows.
+    static_assert(NF >= 1 && NF <= kMaxFold, "new tokens per row");
+    float qv[E];
+    float kv[NF][E];
+    float vv[NF][E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        float a, b;
+        unpack2<BF16>(static_cast<uint32_t>(p.app_q[static_cast<int64_t>(row) * D + lane * E + e]), a, b);
+        qv[e] = a;
+    }
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        if (j < seen) {
+            const int64_t at = ((static_cast<int64_t>(t.b) * n + j) * hk + kvh) * D + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                float a, b;
+                unpack2<BF16>(static_cast<uint32_t>(p.app_k[at + e]) | (static_cast<uint32_t>(p.app_v[at + e]) << 16),
+                              a, b);
+                kv[j][e] = a;
+                vv[j][e] = b;
+            }
+        }
+    }
+    const int32_t raw = p.seqlens[t.b];
+    const RowUnits ru = row_units(p, t.b, lane);
+    float mx = kNegInf;
+    float den = 0.f;
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        acc[e] = 0.f;
+    }
+    if (ru.nb > 0) {
+        const StreamParts sp = stream_parts(p, ru, t.b, t.u);
+        const int64_t lse_stride = static_cast<int64_t>(p.part_heads) << p.gang_shift;
+        merge_parts<E, kBatch>(p.part_lse + sp.slot0 * p.part_heads + t.hn,
+                               p.part_o + (sp.slot0 * p.part_heads + t.hn) * D + lane * E, lse_stride,
+                               lse_stride * D, 0, sp.parts, lane, mx, den, acc);
+    }
+    const int32_t base = uniform(max(raw, 0));
+    float score_log2 = p.app_scale_log2;
+    float v_mul = 1.f;
+    float inv_k = 1.f;
+    float inv_v = 1.f;
+    if constexpr (FP8) {
+        if (p.app_k_scale != nullptr) {
+            score_log2 *= p.app_k_scale[kvh];
+            inv_k = 1.f / p.app_k_scale[kvh];
+        }
+        if (p.app_v_scale != nullptr) {
+            v_mul = p.app_v_scale[kvh];
+            inv_v = 1.f / p.app_v_scale[kvh];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+        const int32_t pos = base + j;
+        if (j >= seen || pos >= p.row_cap) {
+            break;
+        }
+        uint32_t kq = 0;
+        uint32_t vq = 0;
+        if constexpr (FP8) {
+            kq = quantize_e<E>(kv[j], inv_k, kv[j]);
+            vq = quantize_e<E>(vv[j], inv_v, vv[j]);
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            s = fmaf(qv[e], kv[j][e], s);
+        }
+        s = group_sum<64>(s) * score_log2;
+        const float m2 = fmaxf(mx, s);
+        const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
+        const float w = fast_exp2(s - m2);
+        den = den * a + w;
+        mx = m2;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            acc[e] = fmaf(w, vv[j][e] * v_mul, acc[e] * a);
+        }
+        if (i == j && h == kvh * p.group) {
+            const int32_t page = p.app_block_table[static_cast<int64_t>(t.b) * p.app_bt_stride + (pos >> p.page_shift)];
+            if (page >= 0 && page < p.app_num_pages) {
+                const int64_t slot = (static_cast<int64_t>(page) << p.page_shift) | (pos & ((1 << p.page_shift) - 1));
+                const int64_t at = (slot * hk + kvh) * D + lane * E;
+                if constexpr (FP8) {
+                    uint8_t* kc = reinterpret_cast<uint8_t*>(p.app_k_cache);
+                    uint8_t* vc = reinterpret_cast<uint8_t*>(p.app_v_cache);
+                    if constexpr (E == 4) {
+                        *reinterpret_cast<uint32_t*>(kc + at) = kq;
+                        *reinterpret_cast<uint32_t*>(vc + at) = vq;
+                    } else if constexpr (E == 2) {
+                        *reinterpret_cast<uint16_t*>(kc + at) = static_cast<uint16_t>(kq);
+                        *reinterpret_cast<uint16_t*>(vc + at) = static_cast<uint16_t>(vq);
+                    } else {
+                        kc[at] = static_cast<uint8_t>(kq);
+                        vc[at] = static_cast<uint8_t>(vq);
+                    }
+                } else {
+                    const int64_t src = ((static_cast<int64_t>(t.b) * n + j) * hk + kvh) * D + lane * E;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) {
+                        p.app_k_cache[at + e] = p.app_k[src + e];
+                        p.app_v_cache[at + e] = p.app_v[src + e];
+                    }
+                }
+            }
+        }
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        dst[e] = from_f32<BF16>(acc[e] * inv);
+    }
+    if (p.lse != nullptr && lane == 0) {
+        store_lse(p.lse, row, p.q_len, p.num_heads, mx, den);
+    }
+}
+
 // Tile-balanced schedule: row (b, h) belongs to stream u of row b; its parts
 // are located by stream_parts.  One part means the partition already wrote
 // the row; a row without tokens gets zeros; otherwise the partials in slots
 // slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
 // at a time: 16, or for streams of many parts (long rows) as many as 128
 // registers hold, so such a row takes one round trip instead of several.
-template <bool BF16, int D, int kBatch, bool APPEND = false>
+template <bool BF16, int D, int kBatch, int APPEND = 0, int NF = 1>
 __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
     const int lane = threadIdx.x & 63;
@@ -410,8 +597,11 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     }
     const TileRow t = tile_row(p, row);
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
-    if constexpr (APPEND) {
-        combine_append_row<BF16, D, kBatch>(p, t, row, lane, dst);
+    if constexpr (APPEND == 1 && NF == 1) {
+        combine_append_one<BF16, D, kBatch>(p, t, row, lane, dst);
+        return;
+    } else if constexpr (APPEND != 0) { // 1: 16-bit caches, 2: FP8 caches
+        combine_append_row<BF16, D, kBatch, APPEND == 2, NF>(p, t, row, lane, dst);
         return;
     }
 
@@ -719,7 +909,21 @@ static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, c
         constexpr int kLong = 128 / (D / 64) < 64 ? 128 / (D / 64) : 64;
         launch_kernel(combine_tiles_kernel<BF16, D, kLong>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else if (p.tile_workers > 0 && p.app_k != nullptr) {
-        launch_kernel(combine_tiles_kernel<BF16, D, 16, true>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
+        // One new token (the decode step) or up to kMaxFold (the verify step): the
+        // one-token form keeps a single token's registers.
+        const dim3 g(blocks);
+        const dim3 b(64 * kWaves);
+        if (p.app_kv_fp8) {
+            if (p.q_len == 1) {
+                launch_kernel(combine_tiles_kernel<BF16, D, 16, 2, 1>, g, b, 0, stream, ev, p);
+            } else {
+                launch_kernel(combine_tiles_kernel<BF16, D, 16, 2, kMaxFold>, g, b, 0, stream, ev, p);
+            }
+        } else if (p.q_len == 1) {
+            launch_kernel(combine_tiles_kernel<BF16, D, 16, 1, 1>, g, b, 0, stream, ev, p);
+        } else {
+            launch_kernel(combine_tiles_kernel<BF16, D, 16, 1, kMaxFold>, g, b, 0, stream, ev, p);
+        }
     } else if (p.tile_workers > 0) {
         launch_kernel(combine_tiles_kernel<BF16, D, 16>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     } else {

@@ -85,11 +85,12 @@ struct CombineParams {
     int32_t heads_per_wave; // query rows per stream (16 MFMA, 1/2/4 VALU)
     int32_t q_len;        // as in PartitionParams; rows = B * q_len * H
     int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
-    // Decode with a one-token append folded in (app_k != null; tile schedule, one
-    // query token, 16-bit caches, no mask): the partition attended the cached
-    // cache_seqlens[b] tokens and left a partial for every stream; the combine
-    // adds the new token (q . k_new, v_new) to each row and writes k_new / v_new
-    // ([B, 1, Hk, D]) into slot cache_seqlens[b] of the row's block table.
+    // Decode with its append folded in (app_k != null; tile schedule, q_len new
+    // tokens for q_len query tokens, no window, ALiBi or softcap): the partition
+    // attended the cached cache_seqlens[b] tokens and left a partial for every
+    // stream; the combine adds the new tokens each query sees (all, or j <= i
+    // with app_causal) and writes k_new / v_new ([B, q_len, Hk, D]) into slots
+    // cache_seqlens[b] + j of the row's block table (FP8 caches: quantised).
     const uint16_t* app_q;
     const uint16_t* app_k;
     const uint16_t* app_v;
@@ -99,6 +100,10 @@ struct CombineParams {
     int32_t app_bt_stride;
     int32_t app_num_pages;
     float app_scale_log2;
+    int32_t app_causal;
+    int32_t app_kv_fp8;
+    const float* app_k_scale; // FP8 caches: per-KV-head scales, or null (1)
+    const float* app_v_scale;
     float* lse;           // as in PartitionParams
     int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
     int32_t long_rows;    // tile schedule, a row per wave: many parts per stream, all in one round trip

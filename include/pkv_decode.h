@@ -284,10 +284,12 @@ size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_spl
  * shape (two kernels: the partition attends the cached tokens, the combine
  * adds the new token and stores it in the cache), 0 if it launches the append
  * kernel first and then attends the longer rows (three kernels), -1 if desc
- * is invalid.  Folded: one new token, one query token, 16-bit caches, no
- * window or ALiBi, the tile schedule with its row-per-wave combine.  The
- * outputs agree within the decode tolerances (the new token's score is
- * summed in a different order); the caches are written identically.  No
+ * is invalid.  Folded: as many new tokens as query tokens, at most 8 (the
+ * decode step and the speculative verify step, causal or not), 16-bit or
+ * FP8 caches, no window, ALiBi, softcap or rotary tables, the tile schedule
+ * with its row-per-wave combine.  The outputs agree within the decode
+ * tolerances (the new tokens' scores are summed in a different order); the
+ * caches are written identically.  No
  * counterpart in the reference, whose decode never appends
  * (scripts/evaluate_flashattn_submission.py:236-237 passes k = v = None). */
 int pkv_decode_append_folds(const pkv_decode_desc* desc, int num_splits, int64_t seqlen_new);

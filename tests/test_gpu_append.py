@@ -329,3 +329,63 @@ def test_decode_append_folded_full_size(config):
     assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
     diff = (one.float() - two.float()).abs().max().item()
     assert diff < TOL[dtype], diff
+
+
+FOLD_MULTI = [
+    # B, H, Hk, D, P, leading rows, base length, n (= M), causal, dtype, fp8
+    (12, 32, 8, 128, 64, [511, 0, 64, 61], 300, 4, True, 1, False),    # speculative verify, 4 drafts
+    (12, 32, 8, 128, 64, [0, 5, 200], 300, 3, False, 0, False),        # three queries, no mask
+    (12, 32, 8, 128, 64, [511, 0, 64, 63], 300, 1, False, 1, True),    # FP8 decode step
+    (12, 32, 8, 128, 16, [0, 15, 16, 100], 400, 4, True, 0, True),     # FP8 verify
+    (12, 16, 4, 256, 16, [33, 0], 300, 2, True, 1, True),              # FP8, head_dim 256
+]
+
+
+@pytest.mark.parametrize("case", range(len(FOLD_MULTI)))
+def test_decode_append_folded_verify_and_fp8(case):
+    """The folded append with n new tokens for n queries (causal: query i sees drafts j <= i)
+    and with FP8 caches (the drafts quantised as the append kernel stores them): caches bit-exact
+    against the oracle, output and softmax_lse against the fp64 oracle over the appended cache."""
+    import pagedkv
+    from test_gpu_fp8 import assert_close, f32, fp8_cache, from_dev8, to_dev8
+    from test_gpu_lse import assert_lse, lse_buffer
+
+    torch = torch_mod()
+    B, H, Hk, D, P, lead, base, n, causal, dtype, fp8 = FOLD_MULTI[case]
+    announce("decode_append-folded-multi", FOLD_MULTI[case])
+    rng = np.random.default_rng(7100 + case)
+    lens = fold_lens(lead, base, B)
+    q, kc, vc, bt, sl, nk, nv = make_append_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, lens=lens, n=n, dtype=dtype)
+    q = rand_bits(rng, (B, n, H, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=kc.shape[0],
+                             block_table_stride=bt.shape[1], seqlen_q=n, causal=causal,
+                             dtype=pagedkv.PKV_DTYPE_F16 if dtype == 0 else pagedkv.PKV_DTYPE_BF16,
+                             kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME)
+    assert pagedkv.append_folds(desc, 0, n)
+    ks = vs = None
+    if fp8:
+        ks = rng.uniform(0.05, 0.5, Hk).astype(np.float32)
+        vs = rng.uniform(0.05, 0.5, Hk).astype(np.float32)
+        kc, vc = fp8_cache(rng, kc.shape, ks), fp8_cache(rng, vc.shape, vs)
+        want_k, want_v = po.append_kv(kc, vc, bt, sl, po.quantize_e4m3(nk, dtype, ks), po.quantize_e4m3(nv, dtype, vs))
+        want, want_lse = po.attn8_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, n), scale, dtype, k_scale=ks,
+                                      v_scale=vs, causal=causal, lse=True)
+        dk, dv = to_dev8(kc), to_dev8(vc)
+    else:
+        want_k, want_v = po.append_kv(kc, vc, bt, sl, nk, nv)
+        want, want_lse = po.attn_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, n), scale, dtype, causal=causal,
+                                     lse=True)
+        dk, dv = to_dev(kc, dtype), to_dev(vc, dtype)
+    lse = lse_buffer(B, H, n)
+    out = pagedkv.decode(to_dev(q, dtype), dk, dv, i32(bt), i32(sl), scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype), causal=causal, k_scale=f32(ks), v_scale=f32(vs), softmax_lse=lse)
+    torch.cuda.synchronize()
+    if fp8:
+        np.testing.assert_array_equal(from_dev8(dk), want_k)
+        np.testing.assert_array_equal(from_dev8(dv), want_v)
+    else:
+        np.testing.assert_array_equal(from_dev(dk), want_k)
+        np.testing.assert_array_equal(from_dev(dv), want_v)
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
