@@ -135,8 +135,9 @@ typedef struct pkv_decode_desc {
  * With desc->seqlen_q = M > 1 (speculative-decode verify, chunked prefill
  * over a paged cache), each of the M query tokens of a row attends over the
  * keys its mask leaves (causal, sliding window, ALiBi bias; flash-attn 2.6.3
- * semantics); a query with no visible key gets zeros.  M > 1, masks and
- * ALiBi need the MFMA path (PKV_PATH_AUTO or PKV_PATH_MFMA).
+ * semantics); a query with no visible key gets zeros.  M > 1, masks, ALiBi
+ * and a softcap need the MFMA path (PKV_PATH_AUTO or PKV_PATH_MFMA).  With
+ * desc->softmax_lse set, each query row's log-sum-exp is written beside it.
  * Replaces the reference's `extern "C" void run_kernel(...)` launch entry
  * (submission-oj/best_flashattn_kvcache_decode.cu:1186-1201) with the
  * north-star argument order and an explicit stream.
