@@ -124,3 +124,33 @@ def test_rotary_needs_new_keys():
     bt = torch.zeros((1, 4), dtype=torch.int32, device="cuda")
     with pytest.raises(pagedkv.PkvError):
         pagedkv.flash_attn_with_kvcache(q, kc, kc, rotary_cos=cos, rotary_sin=cos, cache_seqlens=3, block_table=bt)
+
+
+def test_flash_attn_argument_errors_are_raised_before_any_launch():
+    """Wrongly shaped or typed rotary tables, softmax_lse buffers and softcaps raise PkvError
+    from the Python layer or the descriptor check, with the caches untouched."""
+    import pagedkv
+
+    torch = torch_mod()
+    announce("flash-attn-argument-errors")
+    q = torch.zeros((2, 1, 8, 64), dtype=torch.bfloat16, device="cuda")
+    kc = torch.randn((8, 16, 2, 64), device="cuda").to(torch.bfloat16)
+    k0 = kc.clone()
+    bt = torch.arange(8, dtype=torch.int32, device="cuda").view(2, 4)
+    sl = torch.tensor([10, 20], dtype=torch.int32, device="cuda")
+    kn = torch.ones((2, 1, 2, 64), dtype=torch.bfloat16, device="cuda")
+    cos = torch.ones((64, 32), dtype=torch.bfloat16, device="cuda")
+    bad = [
+        dict(k=kn, v=kn, rotary_cos=cos.half(), rotary_sin=cos.half()),           # dtype differs from q
+        dict(k=kn, v=kn, rotary_cos=cos, rotary_sin=cos[:, :16]),                  # shapes differ
+        dict(k=kn, v=kn, rotary_cos=cos[:, :4], rotary_sin=cos[:, :4]),            # rotary_dim 8: not a multiple of 16
+        dict(k=kn, v=kn, rotary_cos=cos[:32], rotary_sin=cos[:32]),                # fewer rows than a table row addresses
+        dict(softcap=-1.0),
+    ]
+    for kw in bad:
+        with pytest.raises(pagedkv.PkvError):
+            pagedkv.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=sl, block_table=bt, **kw)
+    with pytest.raises(pagedkv.PkvError):
+        pagedkv.decode(q, kc, kc, bt, sl, softmax_lse=torch.empty((2, 8), dtype=torch.float32, device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.equal(kc.view(torch.int16), k0.view(torch.int16))
