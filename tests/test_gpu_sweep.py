@@ -3,14 +3,15 @@
 Each case draws, from its own seed, the shape (B <= 32, rows up to 4000 tokens, head_dim 64 /
 128 / 256, 1-8 KV heads, group 1-32, page size 1-128, ragged rows with 0- and 1-token rows), the
 dtype, the query tokens (M = 1-8), causal / sliding-window masks, ALiBi slopes ([H] or [B, H]),
-16-bit or FP8 caches with per-KV-head scales, an append of new tokens through k_new / v_new, and
-the split count.  The enumerated tests pin each feature; this sweep looks for interactions none
-of them reaches.
+16-bit or FP8 caches with per-KV-head scales, an append of new tokens through k_new / v_new (the
+folded form where the shape allows it), a score softcap, and the split count; every case also
+returns its softmax_lse.  The enumerated tests pin each feature; this sweep looks for interactions
+none of them reaches.
 
 Bar: the output within TOL + REL * |want| of the fp64 oracle (TOL = 2e-3 fp16 / 1e-2 bf16, REL =
 half an ulp of the output dtype, the rounding of the output itself; masks with ALiBi make outputs
 close to single V rows, where bf16 rounding alone passes 1e-2), and appended cache bytes equal to
-the oracle's bit for bit.
+the oracle's bit for bit; the LSE within 5e-4 + 1e-5 |lse| (+inf where a query sees no key).
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ import pytest
 import pkv_oracle as po
 from conftest import gpu_available, make_case, rand_bits
 from test_gpu_fp8 import assert_close, f32, fp8_cache, from_dev8, i32, to_dev8
+from test_gpu_lse import assert_lse, lse_buffer
 from test_gpu_parity import announce, from_dev, to_dev, torch_mod
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a GPU")]
@@ -57,10 +59,14 @@ def draw(seed: int) -> dict:
     if rs.random() < 0.2:
         H = Hk * G
         alibi = rs.uniform(0.01, 0.3, (B, H) if rs.random() < 0.5 else H).astype(np.float32)
-    return dict(B=B, H=Hk * G, Hk=Hk, D=D, P=P, M=M, lens=lens, n_new=n_new, dtype=int(rs.integers(0, 2)),
-                causal=bool(M > 1 and rs.random() < 0.7), window=window, alibi=alibi,
-                fp8=bool(rs.random() < 0.25), splits=int(rs.choice([0, 0, 1, int(rs.integers(2, 9))])),
-                scale=float(rs.uniform(0.5, 1.5) / math.sqrt(D)))
+    c = dict(B=B, H=Hk * G, Hk=Hk, D=D, P=P, M=M, lens=lens, n_new=n_new, dtype=int(rs.integers(0, 2)),
+             causal=bool(M > 1 and rs.random() < 0.7), window=window, alibi=alibi,
+             fp8=bool(rs.random() < 0.25), splits=int(rs.choice([0, 0, 1, int(rs.integers(2, 9))])),
+             scale=float(rs.uniform(0.5, 1.5) / math.sqrt(D)))
+    # Drawn from a stream of its own, so the fields above keep their values.
+    rs2 = np.random.default_rng(seed + 1_000_003)
+    c["softcap"] = float(rs2.uniform(0.5, 8.0)) if rs2.random() < 0.15 else 0.0
+    return c
 
 
 @pytest.mark.parametrize("case", range(CASES))
@@ -97,16 +103,18 @@ def test_random_feature_mix_matches_oracle(case):
             kc, vc = po.append_kv(kc, vc, bt, lens, nk, nv)
         extra = dict(k_new=to_dev(nk, dtype), v_new=to_dev(nv, dtype))
         seqlens_seen = po.appended_seqlens(lens, n)
+    lse = lse_buffer(B, H, M)
     out = pagedkv.decode(to_dev(q, dtype), kd, vd, i32(bt), i32(lens), c["scale"], c["splits"], causal=c["causal"],
                          window_size=c["window"], alibi_slopes=f32(c["alibi"]), k_scale=f32(ks), v_scale=f32(vs),
-                         **extra)
+                         softcap=c["softcap"], softmax_lse=lse, **extra)
     torch.cuda.synchronize()
-    kw = dict(causal=c["causal"], window=c["window"], alibi=c["alibi"])
+    kw = dict(causal=c["causal"], window=c["window"], alibi=c["alibi"], softcap=c["softcap"], lse=True)
     if c["fp8"]:
-        want = po.attn8_f64(q, kc, vc, bt, seqlens_seen, c["scale"], dtype, k_scale=ks, v_scale=vs, **kw)
+        want, want_lse = po.attn8_f64(q, kc, vc, bt, seqlens_seen, c["scale"], dtype, k_scale=ks, v_scale=vs, **kw)
     else:
-        want = po.attn_f64(q, kc, vc, bt, seqlens_seen, c["scale"], dtype, **kw)
+        want, want_lse = po.attn_f64(q, kc, vc, bt, seqlens_seen, c["scale"], dtype, **kw)
     assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
     if n:
         got_k = from_dev8(kd) if c["fp8"] else from_dev(kd)
         got_v = from_dev8(vd) if c["fp8"] else from_dev(vd)
