@@ -574,22 +574,24 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
         c.head_groups = p.head_groups;
         c.heads_per_wave = r.heads_per_wave;
         c.lse = desc->softmax_lse;
+        pkv::FoldParams f{};
         if (fold != nullptr) {
-            c.app_q = p.q;
-            c.app_k = static_cast<const uint16_t*>(fold->k_new);
-            c.app_v = static_cast<const uint16_t*>(fold->v_new);
-            c.app_k_cache = static_cast<uint16_t*>(fold->k_cache);
-            c.app_v_cache = static_cast<uint16_t*>(fold->v_cache);
-            c.app_block_table = block_table;
-            c.app_bt_stride = p.bt_stride;
-            c.app_num_pages = p.num_pages;
-            c.app_scale_log2 = p.scale_log2;
-            c.app_causal = fold->causal ? 1 : 0;
-            c.app_kv_fp8 = r.kv_fp8 ? 1 : 0;
-            c.app_k_scale = desc->k_scale;
-            c.app_v_scale = desc->v_scale;
+            f.q = p.q;
+            f.k = static_cast<const uint16_t*>(fold->k_new);
+            f.v = static_cast<const uint16_t*>(fold->v_new);
+            f.k_cache = static_cast<uint16_t*>(fold->k_cache);
+            f.v_cache = static_cast<uint16_t*>(fold->v_cache);
+            f.block_table = block_table;
+            f.bt_stride = p.bt_stride;
+            f.num_pages = p.num_pages;
+            f.scale_log2 = p.scale_log2;
+            f.causal = fold->causal ? 1 : 0;
+            f.kv_fp8 = r.kv_fp8 ? 1 : 0;
+            f.k_scale = desc->k_scale;
+            f.v_scale = desc->v_scale;
         }
-        if (pkv::launch_combine(c, bf16, static_cast<int>(r.D), s, comb_ev) != hipSuccess) {
+        if (pkv::launch_combine(c, fold != nullptr ? &f : nullptr, bf16, static_cast<int>(r.D), s, comb_ev) !=
+            hipSuccess) {
             return PKV_ELAUNCH;
         }
     } else if (ev != nullptr) {

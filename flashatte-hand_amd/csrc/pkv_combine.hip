@@ -308,7 +308,7 @@ __device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
 // The decode step's fold on 16-bit caches (one new token, one query token):
 // the general form below with n = 1, written for its registers (the general
 // form needs more and drops the kernel to 3 waves per SIMD at head_dim 256).
-// Row (b, h) of a decode with a one-token append (p.app_k set): the
+// Row (b, h) of a decode with a one-token append (fold arguments f): the
 // partition attended the row's cache_seqlens[b] cached tokens and left every
 // stream's parts in partial slots (force_partial); the new token j = L (its
 // position) joins them here as one more part of weight exp2(s - max), s the
@@ -318,8 +318,8 @@ __device__ __forceinline__ TileRow tile_row(const CombineParams& p, int row) {
 // attended (the append kernel skips it too); a page id outside
 // [0, num_pages) is not written, and the token is attended from k_new.
 template <bool BF16, int D, int kBatch>
-__device__ __forceinline__ void combine_append_one(const CombineParams& p, const TileRow& t, int row, int lane,
-                                                   uint16_t* dst) {
+__device__ __forceinline__ void combine_append_one(const CombineParams& p, const FoldParams& f, const TileRow& t,
+                                                   int row, int lane, uint16_t* dst) {
     constexpr int E = D / 64;
     const int h = row - t.b * p.num_heads;
     const int hk = p.num_heads / p.group;
@@ -330,9 +330,9 @@ __device__ __forceinline__ void combine_append_one(const CombineParams& p, const
     uint16_t kb[E], vb[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const uint16_t qb = p.app_q[static_cast<int64_t>(row) * D + lane * E + e];
-        kb[e] = p.app_k[new_row + e];
-        vb[e] = p.app_v[new_row + e];
+        const uint16_t qb = f.q[static_cast<int64_t>(row) * D + lane * E + e];
+        kb[e] = f.k[new_row + e];
+        vb[e] = f.v[new_row + e];
         float a, b;
         unpack2<BF16>(static_cast<uint32_t>(qb) | (static_cast<uint32_t>(kb[e]) << 16), a, b);
         qv[e] = a;
@@ -364,7 +364,7 @@ __device__ __forceinline__ void combine_append_one(const CombineParams& p, const
         for (int e = 0; e < E; ++e) {
             s = fmaf(qv[e], kv[e], s);
         }
-        s = group_sum<64>(s) * p.app_scale_log2;
+        s = group_sum<64>(s) * f.scale_log2;
         const float m2 = fmaxf(mx, s);
         const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
         const float w = fast_exp2(s - m2);
@@ -375,14 +375,14 @@ __device__ __forceinline__ void combine_append_one(const CombineParams& p, const
             acc[e] = fmaf(w, vv[e], acc[e] * a);
         }
         if (h == kvh * p.group) {
-            const int32_t page = p.app_block_table[static_cast<int64_t>(t.b) * p.app_bt_stride + (L >> p.page_shift)];
-            if (page >= 0 && page < p.app_num_pages) {
+            const int32_t page = f.block_table[static_cast<int64_t>(t.b) * f.bt_stride + (L >> p.page_shift)];
+            if (page >= 0 && page < f.num_pages) {
                 const int64_t slot = (static_cast<int64_t>(page) << p.page_shift) | (L & ((1 << p.page_shift) - 1));
                 const int64_t at = (slot * hk + kvh) * D + lane * E;
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
-                    p.app_k_cache[at + e] = kb[e];
-                    p.app_v_cache[at + e] = vb[e];
+                    f.k_cache[at + e] = kb[e];
+                    f.v_cache[at + e] = vb[e];
                 }
             }
         }
@@ -435,7 +435,7 @@ __device__ __forceinline__ uint32_t quantize_e(const float (&x)[E], float inv, f
 }
 
 // Output row (b, i, h) of a decode whose n = q_len new tokens are folded in
-// (p.app_k set; the speculative-decode form: new token j sits at position
+// (fold arguments f; the speculative-decode form: new token j sits at position
 // L + j, L = max(cache_seqlens[b], 0), and query i at L + i).  The partition
 // attended the row's cached tokens (all of them: every query sits past them)
 // and left every stream's parts in partial slots (force_partial); here the new
@@ -449,8 +449,8 @@ __device__ __forceinline__ uint32_t quantize_e(const float (&x)[E], float inv, f
 // it too); a page id outside [0, num_pages) is not written, and the token is
 // attended from k_new.
 template <bool BF16, int D, int kBatch, bool FP8, int NF>
-__device__ __forceinline__ void combine_append_row(const CombineParams& p, const TileRow& t, int row, int lane,
-                                                   uint16_t* dst) {
+__device__ __forceinline__ void combine_append_row(const CombineParams& p, const FoldParams& f, const TileRow& t,
+                                                   int row, int lane, uint16_t* dst) {
     constexpr int E = D / 64;
     const int n = p.q_len;
     const int per_b = n * p.num_heads;
@@ -458,7 +458,7 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
     const int h = row - t.b * per_b - i * p.num_heads;
     const int hk = p.num_heads / p.group;
     const int kvh = h / p.group;
-    const int seen = p.app_causal ? i + 1 : n; // new tokens query i attends
+    const int seen = f.causal ? i + 1 : n; // new tokens query i attends
     // Loads that do not wait on cache_seqlens: q and the new tokens' rows.
     static_assert(NF >= 1 && NF <= kMaxFold, "new tokens per row");
     float qv[E];
@@ -467,7 +467,7 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         float a, b;
-        unpack2<BF16>(static_cast<uint32_t>(p.app_q[static_cast<int64_t>(row) * D + lane * E + e]), a, b);
+        unpack2<BF16>(static_cast<uint32_t>(f.q[static_cast<int64_t>(row) * D + lane * E + e]), a, b);
         qv[e] = a;
     }
 #pragma unroll
@@ -477,7 +477,7 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float a, b;
-                unpack2<BF16>(static_cast<uint32_t>(p.app_k[at + e]) | (static_cast<uint32_t>(p.app_v[at + e]) << 16),
+                unpack2<BF16>(static_cast<uint32_t>(f.k[at + e]) | (static_cast<uint32_t>(f.v[at + e]) << 16),
                               a, b);
                 kv[j][e] = a;
                 vv[j][e] = b;
@@ -501,18 +501,18 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
                                lse_stride * D, 0, sp.parts, lane, mx, den, acc);
     }
     const int32_t base = uniform(max(raw, 0));
-    float score_log2 = p.app_scale_log2;
+    float score_log2 = f.scale_log2;
     float v_mul = 1.f;
     float inv_k = 1.f;
     float inv_v = 1.f;
     if constexpr (FP8) {
-        if (p.app_k_scale != nullptr) {
-            score_log2 *= p.app_k_scale[kvh];
-            inv_k = 1.f / p.app_k_scale[kvh];
+        if (f.k_scale != nullptr) {
+            score_log2 *= f.k_scale[kvh];
+            inv_k = 1.f / f.k_scale[kvh];
         }
-        if (p.app_v_scale != nullptr) {
-            v_mul = p.app_v_scale[kvh];
-            inv_v = 1.f / p.app_v_scale[kvh];
+        if (f.v_scale != nullptr) {
+            v_mul = f.v_scale[kvh];
+            inv_v = 1.f / f.v_scale[kvh];
         }
     }
 #pragma unroll
@@ -543,13 +543,13 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
             acc[e] = fmaf(w, vv[j][e] * v_mul, acc[e] * a);
         }
         if (i == j && h == kvh * p.group) {
-            const int32_t page = p.app_block_table[static_cast<int64_t>(t.b) * p.app_bt_stride + (pos >> p.page_shift)];
-            if (page >= 0 && page < p.app_num_pages) {
+            const int32_t page = f.block_table[static_cast<int64_t>(t.b) * f.bt_stride + (pos >> p.page_shift)];
+            if (page >= 0 && page < f.num_pages) {
                 const int64_t slot = (static_cast<int64_t>(page) << p.page_shift) | (pos & ((1 << p.page_shift) - 1));
                 const int64_t at = (slot * hk + kvh) * D + lane * E;
                 if constexpr (FP8) {
-                    uint8_t* kc = reinterpret_cast<uint8_t*>(p.app_k_cache);
-                    uint8_t* vc = reinterpret_cast<uint8_t*>(p.app_v_cache);
+                    uint8_t* kc = reinterpret_cast<uint8_t*>(f.k_cache);
+                    uint8_t* vc = reinterpret_cast<uint8_t*>(f.v_cache);
                     if constexpr (E == 4) {
                         *reinterpret_cast<uint32_t*>(kc + at) = kq;
                         *reinterpret_cast<uint32_t*>(vc + at) = vq;
@@ -564,8 +564,8 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
                     const int64_t src = ((static_cast<int64_t>(t.b) * n + j) * hk + kvh) * D + lane * E;
 #pragma unroll
                     for (int e = 0; e < E; ++e) {
-                        p.app_k_cache[at + e] = p.app_k[src + e];
-                        p.app_v_cache[at + e] = p.app_v[src + e];
+                        f.k_cache[at + e] = f.k[src + e];
+                        f.v_cache[at + e] = f.v[src + e];
                     }
                 }
             }
@@ -587,7 +587,9 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
 // slot0, slot0 + G, ... are merged with their LSEs, kBatch partial rows in flight
 // at a time: 16, or for streams of many parts (long rows) as many as 128
 // registers hold, so such a row takes one round trip instead of several.
-template <bool BF16, int D, int kBatch, int APPEND = 0, int NF = 1>
+// LSE: the row's softmax_lse is written when p.lse is set (a kernel without it
+// for the calls that ask for none).
+template <bool BF16, int D, int kBatch, bool LSE>
 __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(CombineParams p) {
     constexpr int E = D / 64;
     const int lane = threadIdx.x & 63;
@@ -597,21 +599,13 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     }
     const TileRow t = tile_row(p, row);
     uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
-    if constexpr (APPEND == 1 && NF == 1) {
-        combine_append_one<BF16, D, kBatch>(p, t, row, lane, dst);
-        return;
-    } else if constexpr (APPEND != 0) { // 1: 16-bit caches, 2: FP8 caches
-        combine_append_row<BF16, D, kBatch, APPEND == 2, NF>(p, t, row, lane, dst);
-        return;
-    }
-
     const RowUnits ru = row_units(p, t.b, lane);
     if (ru.nb == 0) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             dst[e] = 0;
         }
-        if (p.lse != nullptr && lane == 0) {
+        if (LSE && p.lse != nullptr && lane == 0) {
             store_lse(p.lse, row, p.q_len, p.num_heads, 0.f, 0.f);
         }
         return;
@@ -632,8 +626,27 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_tiles_kernel(Combi
     for (int e = 0; e < E; ++e) {
         dst[e] = from_f32<BF16>(acc[e] * inv);
     }
-    if (p.lse != nullptr && lane == 0) {
+    if (LSE && p.lse != nullptr && lane == 0) {
         store_lse(p.lse, row, p.q_len, p.num_heads, mx, den);
+    }
+}
+
+// The tile combine of a decode with its append folded in (fold arguments f):
+// APPEND 1 = 16-bit caches, 2 = FP8 caches; NF new tokens per row at most.
+template <bool BF16, int D, int kBatch, int APPEND, int NF>
+__global__ __launch_bounds__(64 * kCombineWaves) void combine_fold_kernel(CombineParams p, FoldParams f) {
+    constexpr int E = D / 64;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= p.rows) {
+        return;
+    }
+    const TileRow t = tile_row(p, row);
+    uint16_t* dst = p.out + static_cast<int64_t>(row) * D + lane * E;
+    if constexpr (APPEND == 1 && NF == 1) {
+        combine_append_one<BF16, D, kBatch>(p, f, t, row, lane, dst);
+    } else {
+        combine_append_row<BF16, D, kBatch, APPEND == 2, NF>(p, f, t, row, lane, dst);
     }
 }
 
@@ -893,7 +906,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void combine_streams_kernel(Com
 }
 
 template <bool BF16, int D>
-static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, const LaunchEvents& ev) {
+static hipError_t launch_combine_t(const CombineParams& p, const FoldParams* fold, hipStream_t stream,
+                                   const LaunchEvents& ev) {
     constexpr int kWaves = kCombineWaves;
     const int blocks = (p.rows + kWaves - 1) / kWaves;
     if (p.tile_workers > 0 && p.by_stream) {
@@ -907,45 +921,57 @@ static hipError_t launch_combine_t(const CombineParams& p, hipStream_t stream, c
                       stream, ev, p);
     } else if (p.tile_workers > 0 && p.long_rows) {
         constexpr int kLong = 128 / (D / 64) < 64 ? 128 / (D / 64) : 64;
-        launch_kernel(combine_tiles_kernel<BF16, D, kLong>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
-    } else if (p.tile_workers > 0 && p.app_k != nullptr) {
+        if (p.lse != nullptr) {
+            launch_kernel(combine_tiles_kernel<BF16, D, kLong, true>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev,
+                          p);
+        } else {
+            launch_kernel(combine_tiles_kernel<BF16, D, kLong, false>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev,
+                          p);
+        }
+    } else if (p.tile_workers > 0 && fold != nullptr) {
         // One new token (the decode step) or up to kMaxFold (the verify step): the
         // one-token form keeps a single token's registers.
         const dim3 g(blocks);
         const dim3 b(64 * kWaves);
-        if (p.app_kv_fp8) {
+        const FoldParams& f = *fold;
+        if (f.kv_fp8) {
             if (p.q_len == 1) {
-                launch_kernel(combine_tiles_kernel<BF16, D, 16, 2, 1>, g, b, 0, stream, ev, p);
+                launch_kernel(combine_fold_kernel<BF16, D, 16, 2, 1>, g, b, 0, stream, ev, p, f);
             } else {
-                launch_kernel(combine_tiles_kernel<BF16, D, 16, 2, kMaxFold>, g, b, 0, stream, ev, p);
+                launch_kernel(combine_fold_kernel<BF16, D, 16, 2, kMaxFold>, g, b, 0, stream, ev, p, f);
             }
         } else if (p.q_len == 1) {
-            launch_kernel(combine_tiles_kernel<BF16, D, 16, 1, 1>, g, b, 0, stream, ev, p);
+            launch_kernel(combine_fold_kernel<BF16, D, 16, 1, 1>, g, b, 0, stream, ev, p, f);
         } else {
-            launch_kernel(combine_tiles_kernel<BF16, D, 16, 1, kMaxFold>, g, b, 0, stream, ev, p);
+            launch_kernel(combine_fold_kernel<BF16, D, 16, 1, kMaxFold>, g, b, 0, stream, ev, p, f);
         }
     } else if (p.tile_workers > 0) {
-        launch_kernel(combine_tiles_kernel<BF16, D, 16>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
+        if (p.lse != nullptr) {
+            launch_kernel(combine_tiles_kernel<BF16, D, 16, true>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
+        } else {
+            launch_kernel(combine_tiles_kernel<BF16, D, 16, false>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev,
+                          p);
+        }
     } else {
         launch_kernel(combine_kernel<BF16, D>, dim3(blocks), dim3(64 * kWaves), 0, stream, ev, p);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,
-                          const LaunchEvents& ev) {
+hipError_t launch_combine(const CombineParams& p, const FoldParams* fold, bool bf16, int head_dim,
+                          hipStream_t stream, const LaunchEvents& ev) {
     if (bf16) {
         switch (head_dim) {
-        case 64: return launch_combine_t<true, 64>(p, stream, ev);
-        case 128: return launch_combine_t<true, 128>(p, stream, ev);
-        case 256: return launch_combine_t<true, 256>(p, stream, ev);
+        case 64: return launch_combine_t<true, 64>(p, fold, stream, ev);
+        case 128: return launch_combine_t<true, 128>(p, fold, stream, ev);
+        case 256: return launch_combine_t<true, 256>(p, fold, stream, ev);
         default: return hipErrorInvalidValue;
         }
     }
     switch (head_dim) {
-    case 64: return launch_combine_t<false, 64>(p, stream, ev);
-    case 128: return launch_combine_t<false, 128>(p, stream, ev);
-    case 256: return launch_combine_t<false, 256>(p, stream, ev);
+    case 64: return launch_combine_t<false, 64>(p, fold, stream, ev);
+    case 128: return launch_combine_t<false, 128>(p, fold, stream, ev);
+    case 256: return launch_combine_t<false, 256>(p, fold, stream, ev);
     default: return hipErrorInvalidValue;
     }
 }

@@ -85,29 +85,34 @@ struct CombineParams {
     int32_t heads_per_wave; // query rows per stream (16 MFMA, 1/2/4 VALU)
     int32_t q_len;        // as in PartitionParams; rows = B * q_len * H
     int32_t win_left;     // as in PartitionParams (it bounds the tiles a row's streams cover)
-    // Decode with its append folded in (app_k != null; tile schedule, q_len new
-    // tokens for q_len query tokens, no window, ALiBi or softcap): the partition
-    // attended the cached cache_seqlens[b] tokens and left a partial for every
-    // stream; the combine adds the new tokens each query sees (all, or j <= i
-    // with app_causal) and writes k_new / v_new ([B, q_len, Hk, D]) into slots
-    // cache_seqlens[b] + j of the row's block table (FP8 caches: quantised).
-    const uint16_t* app_q;
-    const uint16_t* app_k;
-    const uint16_t* app_v;
-    uint16_t* app_k_cache;
-    uint16_t* app_v_cache;
-    const int32_t* app_block_table;
-    int32_t app_bt_stride;
-    int32_t app_num_pages;
-    float app_scale_log2;
-    int32_t app_causal;
-    int32_t app_kv_fp8;
-    const float* app_k_scale; // FP8 caches: per-KV-head scales, or null (1)
-    const float* app_v_scale;
     float* lse;           // as in PartitionParams
     int32_t by_stream;    // tile schedule: one wave per block of a stream's rows (few parts per stream)
     int32_t long_rows;    // tile schedule, a row per wave: many parts per stream, all in one round trip
     int32_t row_groups;   // tile schedule, a workgroup per row: very many parts per stream (few long rows)
+};
+
+// Decode with its append folded into the combine (tile schedule, q_len new
+// tokens for q_len query tokens, no window, ALiBi or softcap): the partition
+// attended the cached cache_seqlens[b] tokens and left a partial for every
+// stream; the combine adds the new tokens each query sees (all, or j <= i when
+// causal) and writes k_new / v_new ([B, q_len, Hk, D]) into slots
+// cache_seqlens[b] + j of the row's block table (FP8 caches: quantised).  A
+// kernel argument of the fold kernels only, so the plain combine's argument
+// block stays as small as it was without the fold.
+struct FoldParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    const int32_t* block_table;
+    int32_t bt_stride;
+    int32_t num_pages;
+    float scale_log2;
+    int32_t causal;
+    int32_t kv_fp8;
+    const float* k_scale; // FP8 caches: per-KV-head scales, or null (1)
+    const float* v_scale;
 };
 
 // Query rows per wave of the tile schedule's stream combine.
@@ -262,15 +267,18 @@ __device__ __forceinline__ float tanh_f32(float x) {
 // [B, M, H]: (m2 + log2 l) * ln 2 from a log2-domain max m2 and the weight sum
 // l of the row's probabilities exp2(s - m2); +inf for a row that saw no key
 // (flash-attn 2.6.3 writes +inf there; mathematically log 0 = -inf).
+// Rows number B * M * H <= 2^30 (the descriptor check), so the index math is
+// 32-bit.
 __device__ __forceinline__ void store_lse(float* lse, int64_t row, int32_t q_len, int32_t num_heads, float m2,
                                           float l) {
-    int64_t at = row;
+    uint32_t at = static_cast<uint32_t>(row);
     if (q_len > 1) {
-        const int64_t per_b = static_cast<int64_t>(q_len) * num_heads;
-        const int64_t b = row / per_b;
-        const int64_t rem = row - b * per_b;
-        const int64_t i = rem / num_heads;
-        at = (b * num_heads + (rem - i * num_heads)) * q_len + i;
+        const uint32_t nh = static_cast<uint32_t>(num_heads);
+        const uint32_t per_b = static_cast<uint32_t>(q_len) * nh;
+        const uint32_t b = at / per_b;
+        const uint32_t rem = at - b * per_b;
+        const uint32_t i = rem / nh;
+        at = (b * nh + (rem - i * nh)) * static_cast<uint32_t>(q_len) + i;
     }
     lse[at] = l > 0.f ? (m2 + fast_log2(l)) * 0.69314718055994531f : __builtin_huge_valf();
 }

@@ -36,9 +36,10 @@ inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_
 hipError_t launch_partition(const PartitionParams& p, bool mfma, bool bf16, int head_dim, int heads_per_wave,
                             hipStream_t stream, const LaunchEvents& ev);
 
-// LSE combine of split partials into the 16-bit output.
-hipError_t launch_combine(const CombineParams& p, bool bf16, int head_dim, hipStream_t stream,
-                          const LaunchEvents& ev);
+// LSE combine of split partials into the 16-bit output; with `fold` (tile
+// schedule only) the combine also adds and stores the appended tokens.
+hipError_t launch_combine(const CombineParams& p, const FoldParams* fold, bool bf16, int head_dim,
+                          hipStream_t stream, const LaunchEvents& ev);
 
 // Paged KV-cache append: slot-mapping form when p.slot_mapping is set, else
 // the block-table form.

@@ -954,6 +954,11 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             stage_tile<D, FP8, Math::kBF16>(r[d], lds, lane);
+            // The whole tile is staged before the prefetch goes out.  Left to
+            // itself the scheduler may interleave the two (issue part of the
+            // prefetch after the first chunks land): FP8 C2 measured 28.7
+            // against 27.7 µs per partition that way.
+            __builtin_amdgcn_sched_barrier(0);
             ensure_window(t + 16 * DEPTH);
             load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * DEPTH, end, k + d + DEPTH < ntiles, lane, kvh);
             __builtin_amdgcn_sched_barrier(0);
