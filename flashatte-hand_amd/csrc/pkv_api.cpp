@@ -43,7 +43,7 @@ struct Resolved {
     int64_t rows;     // query rows per KV head: M * group
     int win_left;     // -1 = unbounded
     int win_right;    // -1 = unbounded (0 with a causal mask and several query tokens)
-    bool multi_query; // several query tokens, a window or ALiBi: the masked MFMA policy
+    bool multi_query; // several query tokens, a window, ALiBi, softcap or leftpad: the masked MFMA policy
     bool kv_fp8;      // caches hold OCP FP8 e4m3
     int page_shift;
     int heads_per_wave;
@@ -115,7 +115,7 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
         return PKV_EINVAL;
     }
     if ((reinterpret_cast<uintptr_t>(d->softmax_lse) & 3u) != 0 || !(d->softcap >= 0.f) ||
-        !std::isfinite(d->softcap)) {
+        !std::isfinite(d->softcap) || (reinterpret_cast<uintptr_t>(d->cache_leftpad) & 3u) != 0) {
         return PKV_EINVAL;
     }
     // Rotary tables: both or neither; rotary_dim a multiple of 16 within the
@@ -166,7 +166,8 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     if (M == 1) {
         r.win_right = -1;
     }
-    r.multi_query = M > 1 || r.win_left >= 0 || r.win_right >= 0 || d->alibi_slopes != nullptr || d->softcap > 0.f;
+    r.multi_query = M > 1 || r.win_left >= 0 || r.win_right >= 0 || d->alibi_slopes != nullptr || d->softcap > 0.f ||
+                    d->cache_leftpad != nullptr;
     r.page_shift = ilog2(r.P);
     const int64_t row_cap = d->block_table_stride * r.P;
     const int64_t max_seqlen = d->max_seqlen > 0 ? std::min(d->max_seqlen, row_cap) : row_cap;
@@ -429,12 +430,12 @@ struct AppendFold {
 constexpr int64_t kMaxFoldTokens = 8;
 
 // A plan the fold can serve: the tile schedule with its row-per-wave combine,
-// up to kMaxFoldTokens query rows per (b, head), and no window, ALiBi or
-// softcap (the partition runs without masks: every query sits past the cached
-// tokens).
+// up to kMaxFoldTokens query rows per (b, head), and no window, ALiBi, softcap
+// or cache_leftpad (the partition runs without masks: every query sits past
+// the cached tokens).
 bool fold_plan_ok(const Resolved& r, const pkv_decode_desc* d, const SplitPlan& plan) {
     if (plan.schedule != PKV_SCHED_TILES || r.M > kMaxFoldTokens || r.win_left >= 0 || r.win_right >= 0 ||
-        d->alibi_slopes != nullptr || d->softcap > 0.f || r.rotary) {
+        d->alibi_slopes != nullptr || d->softcap > 0.f || d->cache_leftpad != nullptr || r.rotary) {
         return false;
     }
     const CombineForm f = combine_form(r, plan);
@@ -532,6 +533,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.v_scale = desc->v_scale;
     p.lse = desc->softmax_lse;
     p.softcap_log2 = desc->softcap * 1.4426950408889634074f;
+    p.kv_start = desc->cache_leftpad;
 
     const bool bf16 = desc->dtype == PKV_DTYPE_BF16;
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -661,7 +663,7 @@ pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
 
 // The append folds into the combine when the new tokens are the query tokens
 // (seqlen_new = M <= kMaxFoldTokens, the decode step and the speculative
-// verify step), with no window, ALiBi, softcap or rotary tables, on the tile
+// verify step), with no window, ALiBi, softcap, leftpad or rotary tables, on the tile
 // schedule with the row-per-wave combine (a few parts per stream): the
 // partition attends the cached tokens with `*part` = the appended-length
 // descriptor `a` without its causal mask (every query sits past them), the

@@ -61,6 +61,7 @@ struct PartitionParams {
     const float* v_scale;
     float* lse;           // optional fp32 [B, H, M]: natural-log LSE of each output row (store_lse)
     float softcap_log2;   // > 0: every score x (log2 units) becomes softcap_log2 * tanh(x / softcap_log2)
+    const int32_t* kv_start; // optional [B]: keys below kv_start[b] are visible to no query (cache_leftpad)
 };
 
 struct CombineParams {

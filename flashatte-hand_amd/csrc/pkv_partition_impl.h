@@ -361,14 +361,16 @@ struct MfmaMath {
         if constexpr (MQ) {
             int all_lo = 0;
             int all_hi = seqlen;
+            // cache_leftpad: keys below it are padding for every query of the row.
+            const int pad = p.kv_start != nullptr ? min(max(p.kv_start[b], 0), seqlen) : 0;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const int n = 16 * nb + row_lane(lane);
                 const int pos = seqlen - p.q_len + q.qi[nb];
-                int lo = 0;
+                int lo = pad;
                 int hi = seqlen;
                 if (p.win_left >= 0) {
-                    lo = static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0}));
+                    lo = max(lo, static_cast<int>(max(static_cast<int64_t>(pos) - p.win_left, int64_t{0})));
                 }
                 if (p.win_right >= 0) {
                     hi = static_cast<int>(
@@ -1369,7 +1371,8 @@ template <bool BF16, int D>
 static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wave, hipStream_t stream,
                            const LaunchEvents& ev) {
     const bool multi_query =
-        p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr || p.softcap_log2 > 0.f;
+        p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr || p.softcap_log2 > 0.f ||
+        p.kv_start != nullptr;
     if (mfma) {
         // 16 or 32 query rows per wave (heads_per_wave).
         if (heads_per_wave == 32) {

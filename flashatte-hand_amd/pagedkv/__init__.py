@@ -112,6 +112,7 @@ def make_desc(
     rotary_dim: int = 0,
     rotary_interleaved: bool = True,
     softcap: float = 0.0,
+    cache_leftpad: int = 0,
 ) -> PkvDecodeDesc:
     d = PkvDecodeDesc()
     d.batch = batch
@@ -145,6 +146,7 @@ def make_desc(
     d.rotary_dim = rotary_dim
     d.rotary_interleaved = 1 if rotary_interleaved else 0
     d.softcap = softcap
+    d.cache_leftpad = cache_leftpad or None
     return d
 
 
@@ -229,11 +231,16 @@ def decode(
     rotary_sin=None,
     rotary_interleaved: bool = True,
     softcap: float = 0.0,
+    cache_leftpad=None,
 ):
     """Run the decode operator on device tensors; returns ``out`` ([B,M,H,D]).
 
     ``softcap`` > 0 caps each scaled score s to softcap * tanh(s / softcap)
     before the ALiBi bias (flash-attn's softcap).
+
+    ``cache_leftpad`` (int32 ``[B]``, flash-attn's argument) marks row b's
+    keys below ``cache_leftpad[b]`` as padding no query sees; every position
+    (queries, appended tokens, rotary rows) stays as without it.
 
     ``rotary_cos`` / ``rotary_sin`` ([seqlen_ro, rotary_dim / 2], q's dtype;
     with ``k_new``) rotate the new keys at their positions before they are
@@ -298,6 +305,13 @@ def decode(
         if softmax_lse.dtype != torch.float32 or tuple(softmax_lse.shape) != (B, H, M):
             raise PkvError(PKV_EINVAL, "softmax_lse must be fp32 [B, H, M]")
         lse_ptr = softmax_lse.data_ptr()
+    leftpad_ptr = 0
+    if cache_leftpad is not None:
+        _check_cuda("cache_leftpad", cache_leftpad)
+        if cache_leftpad.dtype != torch.int32 or tuple(cache_leftpad.shape) != (B,) or \
+                not cache_leftpad.is_contiguous():
+            raise PkvError(PKV_EINVAL, "cache_leftpad must be a contiguous int32 [B] tensor")
+        leftpad_ptr = cache_leftpad.data_ptr()
     seqlen_new = 0
     if k_new is not None or v_new is not None:
         seqlen_new = _check_new_tokens(k_new, v_new, k_cache, B)
@@ -320,7 +334,7 @@ def decode(
         split_tokens=split_tokens, prof_events=prof_events, seqlen_q=M, causal=causal, window_size=window_size,
         alibi_slopes=alibi_ptr, alibi_batch_stride=alibi_stride, kv_dtype=kv_dtype,
         k_scale=_scale_ptr("k_scale", k_scale, Hk), v_scale=_scale_ptr("v_scale", v_scale, Hk),
-        softmax_lse=lse_ptr, softcap=float(softcap), **rot,
+        softmax_lse=lse_ptr, softcap=float(softcap), cache_leftpad=leftpad_ptr, **rot,
     )
     lib = _lib.load()
     if seqlen_new:
@@ -510,13 +524,15 @@ def flash_attn_with_kvcache(
     ``cache_batch_idx[b]`` (b without it); ``cache_seqlens`` None means every
     row holds seqlen_cache tokens.  They are attended as pages of the largest
     power of two up to 1024 that divides seqlen_cache, through a block table
-    built here (one small device tensor).  ``cache_leftpad`` raises
-    PkvError(PKV_EUNSUPPORTED), and so does ``cache_batch_idx`` with a block
-    table (flash-attn 2.6.3 refuses both with paged caches too).
+    built here (one small device tensor); ``cache_leftpad`` (int32 [B]) marks
+    each row's keys below it as padding that no query sees, positions
+    unchanged.  ``cache_leftpad`` and ``cache_batch_idx`` with a block table
+    raise PkvError(PKV_EUNSUPPORTED) (flash-attn 2.6.3 refuses both with paged
+    caches too).
     """
     torch = _torch()
-    if cache_leftpad is not None:
-        raise PkvError(PKV_EUNSUPPORTED, "cache_leftpad")
+    if cache_leftpad is not None and block_table is not None:
+        raise PkvError(PKV_EUNSUPPORTED, "cache_leftpad with a block table")
     if block_table is None:
         k_cache, v_cache, block_table = _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx)
         if cache_seqlens is None:
@@ -540,7 +556,8 @@ def flash_attn_with_kvcache(
                  alibi_slopes=None if alibi_slopes is None else alibi_slopes.float().contiguous(), softmax_lse=lse,
                  rotary_cos=None if rotary_cos is None else rotary_cos.contiguous(),
                  rotary_sin=None if rotary_sin is None else rotary_sin.contiguous(),
-                 rotary_interleaved=rotary_interleaved, softcap=softcap)
+                 rotary_interleaved=rotary_interleaved, softcap=softcap,
+                 cache_leftpad=None if cache_leftpad is None else cache_leftpad.to(torch.int32).contiguous())
     return (out, lse) if return_softmax_lse else out
 
 

@@ -94,6 +94,7 @@ class PkvDecodeDesc(ctypes.Structure):
         ("rotary_dim", ctypes.c_int32),
         ("rotary_interleaved", ctypes.c_int32),
         ("softcap", ctypes.c_float),
+        ("cache_leftpad", ctypes.c_void_p),
     ]
 
 

@@ -20,7 +20,9 @@
  *                              flash-attn 2.6.3 (setup/pip_full_list.txt:54): query i of M at
  *                              position i + L - M; causal keeps keys j <= pos; a window keeps
  *                              pos - left <= j <= pos + right; ALiBi adds -slope * |pos - j|
- *                              to the scaled score; a query with no visible key gives 0
+ *                              to the scaled score; a query with no visible key gives 0;
+ *                              cache_leftpad (flash-attn 2.6.3's flash_attn_with_kvcache
+ *                              argument) hides the keys below it (kv_start)
  *   pkv_oracle_attn8_f64       the same over OCP FP8 e4m3 caches with per-KV-head scales (no
  *                              counterpart in the reference, which keeps 16-bit caches)
  *   pkv_oracle_e4m3_to_f32     the OCP 8-bit floating point specification's E4M3 encoding
@@ -390,7 +392,8 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
                           const int32_t* block_table, const int32_t* cache_seqlens, int64_t seqlen_q, int causal,
                           int64_t window_left, int64_t window_right, const float* alibi_slopes,
                           int64_t alibi_batch_stride, int kv_fp8, const float* k_scale, const float* v_scale,
-                          double softmax_scale, double* out, double* lse, double softcap) {
+                          double softmax_scale, double* out, double* lse, double softcap,
+                          const int32_t* kv_start) {
     build_f16_table();
     set_threads(d);
     const int64_t B = d->batch, H = d->num_heads, D = d->head_dim, M = seqlen_q;
@@ -416,6 +419,7 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
             const int64_t kvh = h / group;
             const int64_t n = row_seqlen(d, cache_seqlens, b);
             const int64_t pos = i + n - M;
+            const int64_t lo = kv_start ? (int64_t)kv_start[b] : 0; /* cache_leftpad: keys below it are hidden */
             const double slope = alibi_slopes ? (double)alibi_slopes[b * alibi_batch_stride + h] : 0.0;
             const double ks = (kv_fp8 && k_scale) ? (double)k_scale[kvh] : 1.0;
             const double vs = (kv_fp8 && v_scale) ? (double)v_scale[kvh] : 1.0;
@@ -442,7 +446,7 @@ static void attn_f64_impl(const pkv_oracle_dims* d, const uint16_t* q, const voi
             }
             double mx = -INFINITY;
             for (int64_t t = 0; t < n; ++t) {
-                const int visible = (!causal || t <= pos) && (window_left < 0 || t >= pos - window_left) &&
+                const int visible = t >= lo && (!causal || t <= pos) && (window_left < 0 || t >= pos - window_left) &&
                                     (window_right < 0 || t <= pos + window_right);
                 if (!visible) {
                     scores[t] = -INFINITY;
@@ -493,9 +497,9 @@ void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint
                          const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out, double* lse, double softcap) {
+                         double* out, double* lse, double softcap, const int32_t* kv_start) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out, lse, softcap);
+                  alibi_slopes, alibi_batch_stride, 0, NULL, NULL, softmax_scale, out, lse, softcap, kv_start);
 }
 
 void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint8_t* k_cache,
@@ -503,9 +507,9 @@ void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uin
                           int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                           const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
                           const float* v_scale, double softmax_scale, double* out, double* lse,
-                          double softcap) {
+                          double softcap, const int32_t* kv_start) {
     attn_f64_impl(d, q, k_cache, v_cache, block_table, cache_seqlens, seqlen_q, causal, window_left, window_right,
-                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out, lse, softcap);
+                  alibi_slopes, alibi_batch_stride, 1, k_scale, v_scale, softmax_scale, out, lse, softcap, kv_start);
 }
 
 /* ---------------------------------------------------------------- split-KV algebra */

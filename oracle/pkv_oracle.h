@@ -64,12 +64,14 @@ void pkv_oracle_decode_f64(const pkv_oracle_dims* d, const uint16_t* q, const ui
  * query's log(sum over its visible keys of exp(score)), natural log, +inf for
  * a query without a visible key (flash-attn's softmax_lse).  softcap > 0:
  * each scaled score s becomes softcap * tanh(s / softcap) before the ALiBi
- * term (flash-attn 2.6.3's softcap). */
+ * term (flash-attn 2.6.3's softcap).  kv_start (optional int32 [B],
+ * flash-attn's cache_leftpad): keys t < kv_start[b] are visible to no query
+ * of row b; positions are unchanged. */
 void pkv_oracle_attn_f64(const pkv_oracle_dims* d, const uint16_t* q, const uint16_t* k_cache,
                          const uint16_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                          int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                          const float* alibi_slopes, int64_t alibi_batch_stride, double softmax_scale,
-                         double* out, double* lse, double softcap);
+                         double* out, double* lse, double softcap, const int32_t* kv_start);
 
 /* OCP FP8 E4M3 ("e4m3fn": no infinities, S.1111.111 = NaN, max 448) to fp32. */
 float pkv_oracle_e4m3_to_f32(uint8_t b);
@@ -80,7 +82,8 @@ void pkv_oracle_attn8_f64(const pkv_oracle_dims* d, const uint16_t* q, const uin
                           const uint8_t* v_cache, const int32_t* block_table, const int32_t* cache_seqlens,
                           int64_t seqlen_q, int causal, int64_t window_left, int64_t window_right,
                           const float* alibi_slopes, int64_t alibi_batch_stride, const float* k_scale,
-                          const float* v_scale, double softmax_scale, double* out, double* lse, double softcap);
+                          const float* v_scale, double softmax_scale, double* out, double* lse, double softcap,
+                          const int32_t* kv_start);
 
 /* Split-KV partition step (best_flashattn_kvcache_decode.cu:664-697, 782-864):
  * split s of row b covers pages [n*s/S, n*(s+1)/S) of its n valid pages;

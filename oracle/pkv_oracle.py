@@ -70,13 +70,14 @@ def load():
     lib.pkv_oracle_combine_f32.restype = None
     lib.pkv_oracle_attn_f64.argtypes = [dp, _u16p, _u16p, _u16p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
-                                        ctypes.c_double, _f64p, ctypes.c_void_p, ctypes.c_double]
+                                        ctypes.c_double, _f64p, ctypes.c_void_p, ctypes.c_double,
+                                        ctypes.c_void_p]
     lib.pkv_oracle_attn_f64.restype = None
     _u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
     lib.pkv_oracle_attn8_f64.argtypes = [dp, _u16p, _u8p, _u8p, _i32p, _i32p, ctypes.c_int64, ctypes.c_int,
                                          ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double, _f64p, ctypes.c_void_p,
-                                         ctypes.c_double]
+                                         ctypes.c_double, ctypes.c_void_p]
     lib.pkv_oracle_attn8_f64.restype = None
     lib.pkv_oracle_e4m3_to_f32.argtypes = [ctypes.c_uint8]
     lib.pkv_oracle_e4m3_to_f32.restype = ctypes.c_float
@@ -129,19 +130,29 @@ def decode_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, threads=
     return out
 
 
+def _leftpad_ptr(leftpad, B, keep):
+    if leftpad is None:
+        return None
+    a = np.ascontiguousarray(np.broadcast_to(np.asarray(leftpad, dtype=np.int32), (B,)))
+    keep.append(a)
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
 def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=False, window=(-1, -1),
-             alibi=None, threads=0, lse=False, softcap=0.0):
+             alibi=None, threads=0, lse=False, softcap=0.0, leftpad=None):
     """Dense fp64 attention of q [B, M, H, D] with flash-attn 2.6.3 masks; returns float64 [B, M, H, D],
     and with lse=True also the float64 softmax_lse [B, H, M] (natural log, +inf for a query without a
     visible key).  softcap > 0 caps each scaled score s to softcap * tanh(s / softcap) before ALiBi.
 
-    alibi: None, fp32 [H] or [B, H] slopes."""
+    alibi: None, fp32 [H] or [B, H] slopes.  leftpad: None or int32 [B] (flash-attn's cache_leftpad):
+    keys at positions below leftpad[b] are visible to no query of row b."""
     lib = load()
     B, M, H, D = q.shape
     num_pages, P, Hk, _ = k_cache.shape
     d = dims(B, H, Hk, D, P, num_pages, block_table.shape[1], dtype, threads)
     out = np.empty(q.shape, dtype=np.float64)
     lse_out = np.empty((B, H, M), dtype=np.float64) if lse else None
+    keep = []
     slopes = None
     stride = 0
     if alibi is not None:
@@ -152,12 +163,12 @@ def attn_f64(q, k_cache, v_cache, block_table, seqlens, scale, dtype, causal=Fal
                             int(window[0]), int(window[1]),
                             None if slopes is None else slopes.ctypes.data_as(ctypes.c_void_p), int(stride),
                             float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p),
-                            float(softcap))
+                            float(softcap), _leftpad_ptr(leftpad, B, keep))
     return (out, lse_out) if lse else out
 
 
 def attn8_f64(q, k_cache8, v_cache8, block_table, seqlens, scale, dtype, k_scale=None, v_scale=None, causal=False,
-              window=(-1, -1), alibi=None, threads=0, lse=False, softcap=0.0):
+              window=(-1, -1), alibi=None, threads=0, lse=False, softcap=0.0, leftpad=None):
     """attn_f64 over OCP FP8 e4m3 caches (uint8 [num_pages, P, Hk, D]) with per-KV-head fp32 scales."""
     lib = load()
     B, M, H, D = q.shape
@@ -181,7 +192,7 @@ def attn8_f64(q, k_cache8, v_cache8, block_table, seqlens, scale, dtype, k_scale
                              _c(block_table, np.int32), _c(seqlens, np.int32), int(M), int(bool(causal)),
                              int(window[0]), int(window[1]), ptr(alibi), int(stride), ptr(k_scale), ptr(v_scale),
                              float(scale), out, None if lse_out is None else lse_out.ctypes.data_as(ctypes.c_void_p),
-                             float(softcap))
+                             float(softcap), _leftpad_ptr(leftpad, B, keep))
     return (out, lse_out) if lse else out
 
 

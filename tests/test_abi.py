@@ -480,3 +480,36 @@ def test_softcap_needs_the_mfma_path_and_takes_the_masked_policy():
     assert pagedkv.workspace_size(base_desc(softcap=30.0, path=pagedkv.PKV_PATH_VALU), 0) == 0
     lib = _lib.load()
     assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(softcap=30.0)), 0, 1) == 0
+
+
+def test_cache_leftpad_needs_alignment_and_the_mfma_path_and_never_folds():
+    assert pagedkv.workspace_size(base_desc(cache_leftpad=4096 + 2), 0) == 0  # not 4-byte aligned
+    assert pagedkv.workspace_size(base_desc(cache_leftpad=4096), 0) > 0
+    assert pagedkv.workspace_size(base_desc(cache_leftpad=4096, path=pagedkv.PKV_PATH_VALU), 0) == 0
+    lib = _lib.load()
+    assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(cache_leftpad=4096)), 0, 1) == 0
+    assert lib.pkv_decode_path(ctypes.byref(base_desc(cache_leftpad=4096))) == pagedkv.PKV_PATH_MFMA
+
+
+def test_descriptor_layout_matches_the_header(tmp_path):
+    """The ctypes mirror of pkv_decode_desc against the C header: size and every field's offset,
+    read from a C program compiled against include/pkv_decode.h."""
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    fields = [f[0] for f in _lib.PkvDecodeDesc._fields_]
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "pkv_decode.h"', "int main(void) {",
+             '    printf("%zu\\n", sizeof(pkv_decode_desc));']
+    lines += [f'    printf("%zu\\n", offsetof(pkv_decode_desc, {f}));' for f in fields]
+    lines += ["    return 0;", "}"]
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    include = Path(__file__).resolve().parent.parent / "include"
+    subprocess.run([cc, "-std=c11", f"-I{include}", str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_lib.PkvDecodeDesc)
+    assert got[1:] == [getattr(_lib.PkvDecodeDesc, f).offset for f in fields]
