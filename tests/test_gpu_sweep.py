@@ -4,8 +4,8 @@ Each case draws, from its own seed, the shape (B <= 32, rows up to 4000 tokens, 
 128 / 256, 1-8 KV heads, group 1-32, page size 1-128, ragged rows with 0- and 1-token rows), the
 dtype, the query tokens (M = 1-8), causal / sliding-window masks, ALiBi slopes ([H] or [B, H]),
 16-bit or FP8 caches with per-KV-head scales, an append of new tokens through k_new / v_new (the
-folded form where the shape allows it), a score softcap, and the split count; every case also
-returns its softmax_lse.  The enumerated tests pin each feature; this sweep looks for interactions
+folded form where the shape allows it), a score softcap, a cache_leftpad, and the split count;
+every case also returns its softmax_lse.  The enumerated tests pin each feature; this sweep looks for interactions
 none of them reaches.
 
 Bar: the output within TOL + REL * |want| of the fp64 oracle (TOL = 2e-3 fp16 / 1e-2 bf16, REL =
@@ -66,6 +66,11 @@ def draw(seed: int) -> dict:
     # Drawn from a stream of its own, so the fields above keep their values.
     rs2 = np.random.default_rng(seed + 1_000_003)
     c["softcap"] = float(rs2.uniform(0.5, 8.0)) if rs2.random() < 0.15 else 0.0
+    # cache_leftpad (another stream of its own): 0 up to past the row's end.
+    rs3 = np.random.default_rng(seed + 2_000_003)
+    c["leftpad"] = None
+    if rs3.random() < 0.15:
+        c["leftpad"] = np.minimum(rs3.integers(0, lens + 2), lens + 1).astype(np.int32)
     return c
 
 
@@ -106,9 +111,11 @@ def test_random_feature_mix_matches_oracle(case):
     lse = lse_buffer(B, H, M)
     out = pagedkv.decode(to_dev(q, dtype), kd, vd, i32(bt), i32(lens), c["scale"], c["splits"], causal=c["causal"],
                          window_size=c["window"], alibi_slopes=f32(c["alibi"]), k_scale=f32(ks), v_scale=f32(vs),
-                         softcap=c["softcap"], softmax_lse=lse, **extra)
+                         softcap=c["softcap"], softmax_lse=lse,
+                         cache_leftpad=None if c["leftpad"] is None else i32(c["leftpad"]), **extra)
     torch.cuda.synchronize()
-    kw = dict(causal=c["causal"], window=c["window"], alibi=c["alibi"], softcap=c["softcap"], lse=True)
+    kw = dict(causal=c["causal"], window=c["window"], alibi=c["alibi"], softcap=c["softcap"], lse=True,
+              leftpad=c["leftpad"])
     if c["fp8"]:
         want, want_lse = po.attn8_f64(q, kc, vc, bt, seqlens_seen, c["scale"], dtype, k_scale=ks, v_scale=vs, **kw)
     else:
