@@ -15,7 +15,13 @@ shares no code with the C oracle or the HIP kernels:
 The `mask_*` fixtures write out flash-attn 2.6.3's masks for several query tokens
 (the arguments at eval:242-245), the `fp8_*` ones decode E4M3 from its bit fields
 and quantise by nearest-code table search, and the `append_*` ones place the new
-tokens by slot arithmetic — none of it shared with the oracle or the kernels.
+tokens by slot arithmetic — none of it shared with the oracle or the kernels.  The
+`ext_*` ones add flash-attn 2.6.3's other flash_attn_with_kvcache arguments to the
+masked formula: its softcap (softcap * tanh(s / softcap) before ALiBi), its
+cache_leftpad (keys below it hidden, positions kept) and its softmax_lse (natural
+log-sum-exp of each query's visible scores, +inf without one).
+
+Run with fixture names to write only those (the others keep their files).
 
 The reference holds no vectors of its own (its only check is against flash_attn
 on a MetaX GPU), so these fixtures are the repository's frozen anchors.
@@ -23,6 +29,7 @@ Run from anywhere: python tests/golden/make_golden.py
 """
 from __future__ import annotations
 
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -142,11 +149,14 @@ def select_case(dtype):
 
 # ---------------------------------------------------------------- several query tokens, masks, ALiBi
 
-def mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, alibi, kf=None, vf=None):
+def mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, alibi, kf=None, vf=None, softcap=0.0,
+                  leftpad=None, lse_out=None):
     """flash-attn 2.6.3 semantics, written out directly: query i of M sits at position
     pos = i + L - M and sees the keys j < L with pos - left <= j <= pos + right (-1 = unbounded;
-    causal makes right 0); ALiBi subtracts slope * |pos - j| from the scaled score; a query that
-    sees no key returns 0.  kf / vf: dequantised caches (FP8 cases)."""
+    causal makes right 0) and j >= leftpad[b]; a softcap maps the scaled score s to
+    softcap * tanh(s / softcap); ALiBi then subtracts slope * |pos - j|; a query that sees no key
+    returns 0.  kf / vf: dequantised caches (FP8 cases).  lse_out ([B, H, M], filled when given):
+    log of the sum of exp(score) over the visible keys, +inf for a query without one."""
     qf = from_bits(q, dtype)
     kf = from_bits(k, dtype) if kf is None else kf
     vf = from_bits(v, dtype) if vf is None else vf
@@ -157,11 +167,15 @@ def mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, alibi, kf=
     if causal:
         right = 0
     out = np.zeros((B, M, H, D))
+    if lse_out is not None:
+        lse_out[...] = np.inf
     for b in range(B):
         L = int(seqlens[b])
         for i in range(M):
             pos = i + L - M
             lo = 0 if left < 0 else max(0, pos - left)
+            if leftpad is not None:
+                lo = max(lo, int(leftpad[b]))
             hi = L - 1 if right < 0 else min(L - 1, pos + right)
             if L <= 0 or hi < lo:
                 continue
@@ -171,11 +185,15 @@ def mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, alibi, kf=
                 kk = kf[pages, t % P, h // G]
                 vv = vf[pages, t % P, h // G]
                 s = kk @ qf[b, i, h] * scale
+                if softcap > 0:
+                    s = softcap * np.tanh(s / softcap)
                 if alibi is not None:
                     slope = alibi[b, h] if alibi.ndim == 2 else alibi[h]
                     s = s - float(slope) * np.abs(pos - t)
                 p = np.exp(s - s.max())
                 out[b, i, h] = (p / p.sum()) @ vv
+                if lse_out is not None:
+                    lse_out[b, h, i] = s.max() + np.log(p.sum())
     return out
 
 
@@ -199,6 +217,21 @@ def mask_case(name, seed, B, H, Hk, D, P, seqlens, dtype, M, causal, window=(-1,
              expected=mask_expected(q, k, v, bt, seqlens, scale, dtype, causal, window, slopes))
     if slopes is not None:
         c["alibi"] = slopes
+    return c
+
+
+def ext_case(name, seed, B, H, Hk, D, P, seqlens, dtype, M, causal, window=(-1, -1), alibi=None, softcap=0.0,
+             leftpad=None):
+    """A mask case with flash-attn's softcap and cache_leftpad, and its softmax_lse."""
+    c = mask_case(name, seed, B, H, Hk, D, P, seqlens, dtype, M, causal, window, alibi)
+    lse = np.empty((B, H, M))
+    lp = None if leftpad is None else np.asarray(leftpad, dtype=np.int32)
+    c["expected"] = mask_expected(c["q"], c["k"], c["v"], c["block_table"], c["seqlens"], float(c["scale"]), dtype,
+                                  causal, window, c.get("alibi"), softcap=softcap, leftpad=lp, lse_out=lse)
+    c["expected_lse"] = lse
+    c["softcap"] = np.float64(softcap)
+    if lp is not None:
+        c["leftpad"] = lp
     return c
 
 
@@ -310,9 +343,18 @@ def main():
                  causal=True),
         append_case("append_bf16", 401, B=4, Hk=2, D=128, P=16, lens=[0, 15, 16, 70], n=3, dtype="bf16"),
         append_case("append_fp8_f16", 402, B=3, Hk=2, D=64, P=8, lens=[0, 7, 33], n=2, dtype="f16", fp8=True),
+        ext_case("ext_softcap_lse_bf16", 501, B=3, H=16, Hk=4, D=128, P=16, seqlens=[0, 90, 400], dtype="bf16", M=1,
+                 causal=False, softcap=2.0),
+        ext_case("ext_leftpad_causal_f16", 502, B=3, H=8, Hk=2, D=64, P=8, seqlens=[60, 17, 200], dtype="f16", M=3,
+                 causal=True, leftpad=[10, 17, 0]),
+        ext_case("ext_all_bf16", 503, B=2, H=8, Hk=2, D=128, P=32, seqlens=[300, 129], dtype="bf16", M=2,
+                 causal=True, window=(80, 0), alibi="BH", softcap=5.0, leftpad=[150, 3]),
     ]
+    only = set(sys.argv[1:])
     for c in cases:
         name = c.pop("name")
+        if only and name not in only:
+            continue
         np.savez_compressed(HERE / f"{name}.npz", **c)
         print(name, {k: getattr(v, "shape", v) for k, v in c.items()})
 

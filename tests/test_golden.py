@@ -2,7 +2,8 @@
 
 Kinds: one-token decode over 16-bit caches (the unprefixed names), several query tokens with
 causal / window / ALiBi masks (`mask_*`), OCP FP8 e4m3 caches with per-head scales (`fp8_*`),
-and the paged append (`append_*`, 16-bit and FP8).
+the paged append (`append_*`, 16-bit and FP8), and flash-attn's softcap, cache_leftpad and
+softmax_lse on top of the masks (`ext_*`).
 CPU: the oracle reproduces every fixture's expected output (fp64 dense formulas and
 slot arithmetic computed independently at fixture time; closed form for the select cases),
 and the fixtures' table-search E4M3 encoder agrees with the oracle's quantiser.
@@ -25,7 +26,8 @@ ALL = sorted(p.stem for p in GOLDEN.glob("*.npz"))
 MASK = [n for n in ALL if n.startswith("mask_")]
 FP8 = [n for n in ALL if n.startswith("fp8_")]
 APPEND = [n for n in ALL if n.startswith("append_")]
-FIXTURES = [n for n in ALL if n not in MASK + FP8 + APPEND]  # one query token, 16-bit caches
+EXT = [n for n in ALL if n.startswith("ext_")]
+FIXTURES = [n for n in ALL if n not in MASK + FP8 + APPEND + EXT]  # one query token, 16-bit caches
 TOL = {0: 2e-3, 1: 1e-2}
 REL = {0: 2.0 ** -11, 1: 2.0 ** -8}  # half an ulp of the output dtype (its own rounding)
 
@@ -47,7 +49,7 @@ def mask_args(d):
 def test_fixture_set_is_complete():
     assert {"c1", "select_bf16", "select_f16"} <= set(FIXTURES)
     assert len(FIXTURES) >= 7
-    assert len(MASK) >= 3 and len(FP8) >= 2 and len(APPEND) >= 2
+    assert len(MASK) >= 3 and len(FP8) >= 2 and len(APPEND) >= 2 and len(EXT) >= 3
 
 
 @pytest.mark.parametrize("name", MASK)
@@ -56,6 +58,21 @@ def test_oracle_reproduces_mask_fixture(name):
     got = po.attn_f64(d["q"], d["k"], d["v"], d["block_table"], d["seqlens"], d["scale"], d["dtype_code"],
                       **mask_args(d))
     assert np.max(np.abs(got - d["expected"])) < 1e-9
+
+
+def ext_args(d):
+    return dict(mask_args(d), softcap=float(d["softcap"]), leftpad=d.get("leftpad"))
+
+
+@pytest.mark.parametrize("name", EXT)
+def test_oracle_reproduces_ext_fixture(name):
+    d = load(name)
+    got, lse = po.attn_f64(d["q"], d["k"], d["v"], d["block_table"], d["seqlens"], d["scale"], d["dtype_code"],
+                           lse=True, **ext_args(d))
+    assert np.max(np.abs(got - d["expected"])) < 1e-9
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(d["expected_lse"]))
+    finite = np.isfinite(d["expected_lse"])
+    assert np.max(np.abs(lse[finite] - d["expected_lse"][finite])) < 1e-9
 
 
 @pytest.mark.parametrize("name", FP8)
@@ -165,6 +182,32 @@ def test_hip_path_matches_mask_and_fp8_fixtures(name, splits):
                          **extra)
     torch.cuda.synchronize()
     _close(from_dev(out), d["expected"], dt)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+@pytest.mark.parametrize("splits", [0, 1, 3])
+@pytest.mark.parametrize("name", EXT)
+def test_hip_path_matches_ext_fixtures(name, splits):
+    import pagedkv
+    from test_gpu_fp8 import f32, i32
+    from test_gpu_lse import assert_lse, lse_buffer
+    from test_gpu_parity import announce, from_dev, to_dev, torch_mod
+
+    torch = torch_mod()
+    d = load(name)
+    announce("golden", name, "splits", splits)
+    dt = d["dtype_code"]
+    m = ext_args(d)
+    B, M, H, _ = d["q"].shape
+    lse = lse_buffer(B, H, M)
+    out = pagedkv.decode(to_dev(d["q"], dt), to_dev(d["k"], dt), to_dev(d["v"], dt), i32(d["block_table"]),
+                         i32(d["seqlens"]), d["scale"], splits, causal=m["causal"], window_size=m["window"],
+                         alibi_slopes=f32(m["alibi"]), softcap=m["softcap"], softmax_lse=lse,
+                         cache_leftpad=None if m["leftpad"] is None else i32(m["leftpad"]))
+    torch.cuda.synchronize()
+    _close(from_dev(out), d["expected"], dt)
+    assert_lse(lse, d["expected_lse"])
 
 
 @pytest.mark.gpu
