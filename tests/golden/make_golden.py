@@ -19,7 +19,10 @@ tokens by slot arithmetic — none of it shared with the oracle or the kernels. 
 `ext_*` ones add flash-attn 2.6.3's other flash_attn_with_kvcache arguments to the
 masked formula: its softcap (softcap * tanh(s / softcap) before ALiBi), its
 cache_leftpad (keys below it hidden, positions kept) and its softmax_lse (natural
-log-sum-exp of each query's visible scores, +inf without one).
+log-sum-exp of each query's visible scores, +inf without one).  The `rot_*` ones rotate
+the appended keys and q by flash-attn 2.6.3's rotary tables (pair (x0, x1) at angle row
+pos: (x0 c - x1 s, x0 s + x1 c) as fp32 products and sums, rounded to the dtype) and
+expect the caches after the append and the attention over them.
 
 Run with fixture names to write only those (the others keep their files).
 
@@ -323,6 +326,57 @@ def append_case(name, seed, B, Hk, D, P, lens, n, dtype, fp8=False):
     return c
 
 
+def rotate(x_bits, cos_bits, sin_bits, pos, rd, interleaved, dtype):
+    """x [..., D] bits rotated at table rows pos (broadcast over x's leading dims but the last)."""
+    x = from_bits(x_bits, dtype).astype(np.float32)
+    c = from_bits(cos_bits, dtype).astype(np.float32)[pos]
+    s = from_bits(sin_bits, dtype).astype(np.float32)[pos]
+    out = x.copy()
+    for a in range(rd // 2):
+        i0, i1 = (2 * a, 2 * a + 1) if interleaved else (a, a + rd // 2)
+        ca, sa = c[..., a], s[..., a]
+        x0, x1 = x[..., i0], x[..., i1]
+        out[..., i0] = np.subtract(np.multiply(x0, ca, dtype=np.float32), np.multiply(x1, sa, dtype=np.float32),
+                                   dtype=np.float32)
+        out[..., i1] = np.add(np.multiply(x0, sa, dtype=np.float32), np.multiply(x1, ca, dtype=np.float32),
+                              dtype=np.float32)
+    return to_bits(out, dtype)
+
+
+def rot_case(name, seed, B, H, Hk, D, P, lens, n, dtype, rd, interleaved, causal):
+    """Append of n rotated new tokens per row, then attention of n rotated queries (query i at
+    lens + i when causal, else every query at lens; key j at lens + j)."""
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int32)
+    pages = (lens + n + P - 1) // P
+    pool = int(pages.sum()) + 2
+    stride = int(pages.max())
+    bt = scattered_table(rng, lens + n, P, pool, stride)
+    rows = stride * P
+    ang = np.arange(rows)[:, None] * (10000.0 ** (-np.arange(0, rd, 2) / rd))[None, :]
+    cos, sin = to_bits(np.cos(ang), dtype), to_bits(np.sin(ang), dtype)
+    q = to_bits(rng.standard_normal((B, n, H, D)), dtype)
+    nk = to_bits(rng.standard_normal((B, n, Hk, D)), dtype)
+    nv = to_bits(rng.standard_normal((B, n, Hk, D)), dtype)
+    kc = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+    vc = to_bits(rng.standard_normal((pool, P, Hk, D)), dtype)
+    kpos = lens[:, None] + np.arange(n)[None, :]
+    qpos = kpos if causal else np.repeat(lens[:, None], n, axis=1)
+    rk = rotate(nk, cos, sin, kpos[:, :, None], rd, interleaved, dtype)
+    rq = rotate(q, cos, sin, qpos[:, :, None], rd, interleaved, dtype)
+    ek, ev = kc.copy(), vc.copy()
+    for b in range(B):
+        for j in range(n):
+            pos = int(lens[b]) + j
+            ek[bt[b, pos // P], pos % P] = rk[b, j]
+            ev[bt[b, pos // P], pos % P] = nv[b, j]
+    scale = 1.0 / np.sqrt(D)
+    return dict(name=name, q=q, k_cache=kc, v_cache=vc, k_new=nk, v_new=nv, block_table=bt, seqlens=lens,
+                rotary_cos=cos, rotary_sin=sin, interleaved=np.bool_(interleaved), causal=np.bool_(causal),
+                scale=np.float64(scale), dtype=dtype, expected_k=ek, expected_v=ev,
+                expected=mask_expected(rq, ek, ev, bt, lens + n, scale, dtype, causal, (-1, -1), None))
+
+
 def main():
     cases = [
         c1_case(),
@@ -349,6 +403,10 @@ def main():
                  causal=True, leftpad=[10, 17, 0]),
         ext_case("ext_all_bf16", 503, B=2, H=8, Hk=2, D=128, P=32, seqlens=[300, 129], dtype="bf16", M=2,
                  causal=True, window=(80, 0), alibi="BH", softcap=5.0, leftpad=[150, 3]),
+        rot_case("rot_neox_bf16", 601, B=3, H=16, Hk=4, D=128, P=16, lens=[0, 40, 333], n=1, dtype="bf16", rd=128,
+                 interleaved=False, causal=False),
+        rot_case("rot_interleaved_causal_f16", 602, B=2, H=8, Hk=2, D=128, P=32, lens=[70, 9], n=3, dtype="f16",
+                 rd=64, interleaved=True, causal=True),
     ]
     only = set(sys.argv[1:])
     for c in cases:

@@ -2,8 +2,9 @@
 
 Kinds: one-token decode over 16-bit caches (the unprefixed names), several query tokens with
 causal / window / ALiBi masks (`mask_*`), OCP FP8 e4m3 caches with per-head scales (`fp8_*`),
-the paged append (`append_*`, 16-bit and FP8), and flash-attn's softcap, cache_leftpad and
-softmax_lse on top of the masks (`ext_*`).
+the paged append (`append_*`, 16-bit and FP8), flash-attn's softcap, cache_leftpad and
+softmax_lse on top of the masks (`ext_*`), and its rotary embedding of appended keys and q
+(`rot_*`).
 CPU: the oracle reproduces every fixture's expected output (fp64 dense formulas and
 slot arithmetic computed independently at fixture time; closed form for the select cases),
 and the fixtures' table-search E4M3 encoder agrees with the oracle's quantiser.
@@ -27,7 +28,8 @@ MASK = [n for n in ALL if n.startswith("mask_")]
 FP8 = [n for n in ALL if n.startswith("fp8_")]
 APPEND = [n for n in ALL if n.startswith("append_")]
 EXT = [n for n in ALL if n.startswith("ext_")]
-FIXTURES = [n for n in ALL if n not in MASK + FP8 + APPEND + EXT]  # one query token, 16-bit caches
+ROT = [n for n in ALL if n.startswith("rot_")]
+FIXTURES = [n for n in ALL if n not in MASK + FP8 + APPEND + EXT + ROT]  # one query token, 16-bit caches
 TOL = {0: 2e-3, 1: 1e-2}
 REL = {0: 2.0 ** -11, 1: 2.0 ** -8}  # half an ulp of the output dtype (its own rounding)
 
@@ -49,7 +51,7 @@ def mask_args(d):
 def test_fixture_set_is_complete():
     assert {"c1", "select_bf16", "select_f16"} <= set(FIXTURES)
     assert len(FIXTURES) >= 7
-    assert len(MASK) >= 3 and len(FP8) >= 2 and len(APPEND) >= 2 and len(EXT) >= 3
+    assert len(MASK) >= 3 and len(FP8) >= 2 and len(APPEND) >= 2 and len(EXT) >= 3 and len(ROT) >= 2
 
 
 @pytest.mark.parametrize("name", MASK)
@@ -73,6 +75,31 @@ def test_oracle_reproduces_ext_fixture(name):
     np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(d["expected_lse"]))
     finite = np.isfinite(d["expected_lse"])
     assert np.max(np.abs(lse[finite] - d["expected_lse"][finite])) < 1e-9
+
+
+def rot_oracle(d):
+    """The oracle's rotary, append and attention over a rot_* fixture's inputs."""
+    dt = d["dtype_code"]
+    n = d["k_new"].shape[1]
+    rd = 2 * d["rotary_cos"].shape[1]
+    inter, causal = bool(d["interleaved"]), bool(d["causal"])
+    kpos = po.rotary_positions(d["seqlens"], n, True)
+    qpos = po.rotary_positions(d["seqlens"], n, causal)
+    rk = po.rotary(d["k_new"], d["rotary_cos"], d["rotary_sin"], kpos[:, :, None], rd, inter, dt)
+    rq = po.rotary(d["q"], d["rotary_cos"], d["rotary_sin"], qpos[:, :, None], rd, inter, dt)
+    k, v = po.append_kv(d["k_cache"], d["v_cache"], d["block_table"], d["seqlens"], rk, d["v_new"])
+    out = po.attn_f64(rq, k, v, d["block_table"], po.appended_seqlens(d["seqlens"], n), d["scale"], dt,
+                      causal=causal)
+    return k, v, out
+
+
+@pytest.mark.parametrize("name", ROT)
+def test_oracle_reproduces_rotary_fixture(name):
+    d = load(name)
+    k, v, out = rot_oracle(d)
+    np.testing.assert_array_equal(k, d["expected_k"])
+    np.testing.assert_array_equal(v, d["expected_v"])
+    assert np.max(np.abs(out - d["expected"])) < 1e-9
 
 
 @pytest.mark.parametrize("name", FP8)
@@ -208,6 +235,31 @@ def test_hip_path_matches_ext_fixtures(name, splits):
     torch.cuda.synchronize()
     _close(from_dev(out), d["expected"], dt)
     assert_lse(lse, d["expected_lse"])
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a GPU")
+@pytest.mark.parametrize("splits", [0, 1])
+@pytest.mark.parametrize("name", ROT)
+def test_hip_rotary_append_matches_fixture(name, splits):
+    import pagedkv
+    from test_gpu_fp8 import i32
+    from test_gpu_parity import announce, from_dev, to_dev, torch_mod
+
+    torch = torch_mod()
+    d = load(name)
+    announce("golden", name, "splits", splits)
+    dt = d["dtype_code"]
+    kc, vc = to_dev(d["k_cache"], dt), to_dev(d["v_cache"], dt)
+    out = pagedkv.flash_attn_with_kvcache(
+        to_dev(d["q"], dt), kc, vc, to_dev(d["k_new"], dt), to_dev(d["v_new"], dt),
+        rotary_cos=to_dev(d["rotary_cos"], dt), rotary_sin=to_dev(d["rotary_sin"], dt),
+        cache_seqlens=i32(d["seqlens"]), block_table=i32(d["block_table"]), softmax_scale=d["scale"],
+        causal=bool(d["causal"]), rotary_interleaved=bool(d["interleaved"]), num_splits=splits)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev(kc), d["expected_k"])
+    np.testing.assert_array_equal(from_dev(vc), d["expected_v"])
+    _close(from_dev(out), d["expected"], dt)
 
 
 @pytest.mark.gpu
