@@ -455,6 +455,13 @@ def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, *,
         raise PkvError(st, "pkv_reshape_and_cache")
 
 
+# Block tables built for contiguous caches without cache_batch_idx, by (device, B, rows per
+# cache row): the same table serves every call of a decode loop, so it is built once instead
+# of with a few small kernel launches per call.  Never written or freed once cached (at most
+# 64 of them; further shapes get a table per call).
+_IDENTITY_TABLES: dict = {}
+
+
 def _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx):
     """flash-attn's contiguous caches [B_cache, S, Hk, D] as a paged pool: pages of P tokens
     (the largest power of two up to 1024 dividing S), row b of the batch on the pages of cache
@@ -473,7 +480,13 @@ def _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx):
     if cache_batch_idx is None:
         if b_cache < B:
             raise PkvError(PKV_EINVAL, "k_cache has fewer rows than the batch")
-        rows = torch.arange(B, dtype=torch.int64, device=q.device)
+        key = (str(q.device), B, per_row)
+        table = _IDENTITY_TABLES.get(key)
+        if table is None:
+            table = torch.arange(B * per_row, dtype=torch.int32, device=q.device).view(B, per_row)
+            if len(_IDENTITY_TABLES) < 64:
+                _IDENTITY_TABLES[key] = table
+        return (k_cache.view(b_cache * per_row, P, Hk, D), v_cache.view(b_cache * per_row, P, Hk, D), table)
     else:
         _check_cuda("cache_batch_idx", cache_batch_idx)
         if cache_batch_idx.dim() != 1 or cache_batch_idx.shape[0] != B:
