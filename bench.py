@@ -132,6 +132,10 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         # Several query tokens per row (speculative-decode verify): q / out [B, M, H, D].
         for s_ in sets:
             s_["q"] = torch.randn((cfg.batch, M, cfg.num_heads, cfg.head_dim), device="cuda").to(s_["q"].dtype)
+    if args.leftpad > 0:
+        # cache_leftpad: the first min(leftpad, row length) keys of every row are padding.
+        for s_ in sets:
+            s_["leftpad"] = torch.clamp(s_["cache_seqlens"], max=args.leftpad).to(torch.int32).contiguous()
     torch.cuda.synchronize()
     dev = torch.device("cuda")
     stream = torch.cuda.current_stream(dev)
@@ -147,6 +151,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
         k_scale=base["k_scale"].data_ptr() if fp8 else 0, v_scale=base["v_scale"].data_ptr() if fp8 else 0,
         softcap=args.softcap,
+        cache_leftpad=base["leftpad"].data_ptr() if args.leftpad > 0 else 0,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     splits = pagedkv.num_splits_for(desc, splits_req)
@@ -170,6 +175,8 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
         if fp8:
             desc.k_scale = sets[i % len(sets)]["k_scale"].data_ptr()
             desc.v_scale = sets[i % len(sets)]["v_scale"].data_ptr()
+        if args.leftpad > 0:
+            desc.cache_leftpad = sets[i % len(sets)]["leftpad"].data_ptr()
         st = lib.pkv_decode(q, k, v, bt, sl, scale, splits_req, o, ctypes.byref(desc), sh)
         if st != 0:
             raise pagedkv.PkvError(st)
@@ -229,7 +236,7 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     part_avg_ms = sum(part_ms) / K
     achieved = part_alg / (part_avg_ms * 1e-3) / 1e9
     # The committed counter summaries are for the one-query, unmasked decode (16-bit or FP8 caches).
-    plain = M == 1 and tuple(args.window) == (-1, -1)
+    plain = M == 1 and tuple(args.window) == (-1, -1) and args.softcap == 0 and args.leftpad == 0
     kind = ("mfma" if path == pagedkv.PKV_PATH_MFMA else "valu") + ("_fp8" if fp8 else "")
     traffic = load_traffic(name, kind) if plain else None
     res = {
@@ -476,6 +483,8 @@ def main() -> int:
     ap.add_argument("--causal", action="store_true", help="causal mask (decode op, with --seqlen-q > 1)")
     ap.add_argument("--window", type=int, nargs=2, default=(-1, -1), metavar=("LEFT", "RIGHT"),
                     help="sliding window (decode op); -1 = unbounded")
+    ap.add_argument("--leftpad", type=int, default=0,
+                    help="cache_leftpad (decode op): the first N keys of every row are padding (read and masked)")
     ap.add_argument("--softcap", type=float, default=0.0,
                     help="score softcap (decode op): softcap * tanh(s / softcap), flash-attn's softcap")
     ap.add_argument("--kv", choices=("same", "fp8"), default="same",
@@ -538,7 +547,8 @@ def main() -> int:
                        **({"seqlen_q": args.seqlen_q, "causal": args.causal} if args.seqlen_q > 1 else {}),
                        **({"window": list(args.window)} if tuple(args.window) != (-1, -1) else {}),
                        **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {}),
-                       **({"softcap": args.softcap} if args.softcap > 0 else {})},
+                       **({"softcap": args.softcap} if args.softcap > 0 else {}),
+                       **({"cache_leftpad": args.leftpad} if args.leftpad > 0 else {})},
             "us_per_call": round(res["ms_per_step"] * 1e3, 2),
             "us_p10_p50_p90": [round(res["us_p10"], 2), round(res["us_p50"], 2), round(res["us_p90"], 2)],
             "us_spread": res["spread"],
@@ -551,7 +561,7 @@ def main() -> int:
         }
         # The CPU baseline restates the reference's own path: 16-bit caches, one query token.
         if name == args.config and not args.no_cpu and args.kv == "same" and args.seqlen_q == 1 and \
-                args.softcap == 0:
+                args.softcap == 0 and args.leftpad == 0:
             line["cpu_baseline"] = cpu_baseline(res, torch, args.cpu_budget)
         res.pop("host_arrays", None)
         lines.append(line)
