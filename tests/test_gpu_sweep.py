@@ -82,8 +82,9 @@ def test_random_feature_mix_matches_oracle(case):
     c = draw(7000 + case)
     B, H, Hk, D, P, M, n, dtype = c["B"], c["H"], c["Hk"], c["D"], c["P"], c["M"], c["n_new"], c["dtype"]
     lens = c["lens"]
-    announce("sweep", case, {k: (v.tolist() if isinstance(v, np.ndarray) and v.ndim == 1 and k == "lens" else
-                                 v if not isinstance(v, np.ndarray) else f"slopes{v.shape}") for k, v in c.items()})
+    announce("sweep", case, {k: (v.tolist() if isinstance(v, np.ndarray) and v.ndim == 1 and k in ("lens", "leftpad")
+                                 else v if not isinstance(v, np.ndarray) else f"slopes{v.shape}")
+                             for k, v in c.items()})
     rng = np.random.default_rng(9000 + case)
     # Pages for the rows after the append; unused table entries stay -1.
     _, k16, v16, bt, _ = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=lens + n, dtype=dtype)
