@@ -157,3 +157,30 @@ def test_leftpad_argument_errors():
     for bad in (sl.long(), sl[:1], torch.zeros((2, 1), dtype=torch.int32, device="cuda")):
         with pytest.raises(pagedkv.PkvError):
             pagedkv.decode(q, kc, kc, bt, sl, cache_leftpad=bad)
+
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+def test_full_size_config_with_leftpad_and_softcap(name):
+    """The BASELINE config at full size with a cache_leftpad of 0-1000 tokens per row (rows padded
+    to their end included) and a softcap of 30, on the heuristic schedule (the tile schedule with
+    its gangs and combine forms): every output row and its LSE against the fp64 oracle."""
+    import pagedkv
+    from pagedkv.configs import make_config, make_tensors
+
+    torch = torch_mod()
+    cfg = make_config(name)
+    announce("leftpad-full", name, cfg.describe())
+    t = make_tensors(cfg, "cuda")
+    dt = 0 if cfg.dtype == "f16" else 1
+    rng = np.random.default_rng(7400)
+    lp = np.minimum(rng.integers(0, 1001, cfg.batch), cfg.seqlens).astype(np.int32)
+    lp[: max(1, cfg.batch // 16)] = cfg.seqlens[: max(1, cfg.batch // 16)]  # a few rows all padding
+    lse = lse_buffer(cfg.batch, cfg.num_heads, 1)
+    out = pagedkv.decode(t["q"], t["k_cache"], t["v_cache"], t["block_table"], t["cache_seqlens"], cfg.scale, 0,
+                         max_seqlen=int(cfg.seqlens.max()), softmax_lse=lse, softcap=30.0, cache_leftpad=i32(lp))
+    torch.cuda.synchronize()
+    announce("leftpad-full", name, "fp64 oracle over all", cfg.batch * cfg.num_heads, "rows")
+    want, want_lse = po.attn_f64(from_dev(t["q"]), from_dev(t["k_cache"]), from_dev(t["v_cache"]), cfg.block_table,
+                                 cfg.seqlens, cfg.scale, dt, lse=True, softcap=30.0, leftpad=lp)
+    assert_close(out, want, dt)
+    assert_lse(lse, want_lse)
