@@ -1,7 +1,7 @@
-"""The BASELINE configs at full size with FP8 caches, and the C2 / C4 shapes as a speculative
-verify step (four causal query tokens), on the heuristic schedule: every output row and its
-softmax_lse against the fp64 oracle (OpenMP over rows on the host), as
-tests/test_gpu_parity.py checks the 16-bit one-token decode.
+"""The BASELINE configs at full size with FP8 caches, the C2 / C4 shapes as a speculative
+verify step (four causal query tokens), and C2 / C5 with a sliding window and ALiBi, on the
+heuristic schedule: every output row and its softmax_lse against the fp64 oracle (OpenMP over
+rows on the host), as tests/test_gpu_parity.py checks the 16-bit one-token decode.
 
 FP8 caches hold the configs' values quantised on the device with per-KV-head scales (torch's
 float8_e4m3fn conversion); the oracle reads the same bytes.  Bar: the decode tolerance plus
@@ -69,5 +69,30 @@ def test_full_size_config_as_causal_verify_step(name):
     announce("verify-full", name, "fp64 oracle over all", cfg.batch * M * cfg.num_heads, "rows")
     want, want_lse = po.attn_f64(from_dev(q), from_dev(t["k_cache"]), from_dev(t["v_cache"]), cfg.block_table,
                                  cfg.seqlens, cfg.scale, dt, causal=True, lse=True)
+    assert_close(out, want, dt)
+    assert_lse(lse, want_lse)
+
+
+@pytest.mark.parametrize("name", ["c2", "c5"])
+def test_full_size_config_with_window_and_alibi(name):
+    """A 1024-token sliding window (which sends the call to the single pass, the window bounding
+    every row) with [B, H] ALiBi slopes."""
+    import pagedkv
+    from pagedkv.configs import make_config, make_tensors
+
+    torch = torch_mod()
+    cfg = make_config(name)
+    announce("window-full", name, cfg.describe())
+    t = make_tensors(cfg, "cuda")
+    dt = 0 if cfg.dtype == "f16" else 1
+    slopes = np.random.default_rng(7700).uniform(0.001, 0.05, (cfg.batch, cfg.num_heads)).astype(np.float32)
+    lse = lse_buffer(cfg.batch, cfg.num_heads, 1)
+    out = pagedkv.decode(t["q"], t["k_cache"], t["v_cache"], t["block_table"], t["cache_seqlens"], cfg.scale, 0,
+                         max_seqlen=int(cfg.seqlens.max()), window_size=(1024, 0),
+                         alibi_slopes=torch.from_numpy(slopes).cuda(), softmax_lse=lse)
+    torch.cuda.synchronize()
+    announce("window-full", name, "fp64 oracle over all", cfg.batch * cfg.num_heads, "rows")
+    want, want_lse = po.attn_f64(from_dev(t["q"]), from_dev(t["k_cache"]), from_dev(t["v_cache"]), cfg.block_table,
+                                 cfg.seqlens, cfg.scale, dt, window=(1024, 0), alibi=slopes, lse=True)
     assert_close(out, want, dt)
     assert_lse(lse, want_lse)
