@@ -430,12 +430,13 @@ struct AppendFold {
 constexpr int64_t kMaxFoldTokens = 8;
 
 // A plan the fold can serve: the tile schedule with its row-per-wave combine,
-// up to kMaxFoldTokens query rows per (b, head), and no window, ALiBi, softcap
-// or cache_leftpad (the partition runs without masks: every query sits past
-// the cached tokens).
+// up to kMaxFoldTokens query rows per (b, head), and no window, ALiBi or
+// softcap (the partition runs without those masks: every query sits past the
+// cached tokens; a cache_leftpad hides the same keys from every query, so the
+// partition applies it and the combine skips new tokens below it).
 bool fold_plan_ok(const Resolved& r, const pkv_decode_desc* d, const SplitPlan& plan) {
     if (plan.schedule != PKV_SCHED_TILES || r.M > kMaxFoldTokens || r.win_left >= 0 || r.win_right >= 0 ||
-        d->alibi_slopes != nullptr || d->softcap > 0.f || d->cache_leftpad != nullptr || r.rotary) {
+        d->alibi_slopes != nullptr || d->softcap > 0.f || r.rotary) {
         return false;
     }
     const CombineForm f = combine_form(r, plan);
@@ -591,6 +592,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
             f.kv_fp8 = r.kv_fp8 ? 1 : 0;
             f.k_scale = desc->k_scale;
             f.v_scale = desc->v_scale;
+            f.kv_start = desc->cache_leftpad;
         }
         if (pkv::launch_combine(c, fold != nullptr ? &f : nullptr, bf16, static_cast<int>(r.D), s, comb_ev) !=
             hipSuccess) {
@@ -663,7 +665,7 @@ pkv_decode_desc appended_desc(const pkv_decode_desc* d, int64_t seqlen_new) {
 
 // The append folds into the combine when the new tokens are the query tokens
 // (seqlen_new = M <= kMaxFoldTokens, the decode step and the speculative
-// verify step), with no window, ALiBi, softcap, leftpad or rotary tables, on the tile
+// verify step), with no window, ALiBi, softcap or rotary tables, on the tile
 // schedule with the row-per-wave combine (a few parts per stream): the
 // partition attends the cached tokens with `*part` = the appended-length
 // descriptor `a` without its causal mask (every query sits past them), the

@@ -359,20 +359,23 @@ __device__ __forceinline__ void combine_append_one(const CombineParams& p, const
     const int32_t raw = p.seqlens[t.b];
     const bool fits = uniform(max(raw, 0)) < p.row_cap;
     if (fits) {
-        float s = 0.f;
+        // cache_leftpad at or past the new token's position hides it from the query.
+        if (f.kv_start == nullptr || L >= uniform(f.kv_start[t.b])) {
+            float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s = fmaf(qv[e], kv[e], s);
-        }
-        s = group_sum<64>(s) * f.scale_log2;
-        const float m2 = fmaxf(mx, s);
-        const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
-        const float w = fast_exp2(s - m2);
-        den = den * a + w;
-        mx = m2;
+            for (int e = 0; e < E; ++e) {
+                s = fmaf(qv[e], kv[e], s);
+            }
+            s = group_sum<64>(s) * f.scale_log2;
+            const float m2 = fmaxf(mx, s);
+            const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
+            const float w = fast_exp2(s - m2);
+            den = den * a + w;
+            mx = m2;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            acc[e] = fmaf(w, vv[e], acc[e] * a);
+            for (int e = 0; e < E; ++e) {
+                acc[e] = fmaf(w, vv[e], acc[e] * a);
+            }
         }
         if (h == kvh * p.group) {
             const int32_t page = f.block_table[static_cast<int64_t>(t.b) * f.bt_stride + (L >> p.page_shift)];
@@ -515,6 +518,8 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
             inv_v = 1.f / f.v_scale[kvh];
         }
     }
+    // cache_leftpad: new tokens below it are stored but attended by no query.
+    const int32_t pad = f.kv_start != nullptr ? uniform(f.kv_start[t.b]) : 0;
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
         const int32_t pos = base + j;
@@ -527,20 +532,22 @@ __device__ __forceinline__ void combine_append_row(const CombineParams& p, const
             kq = quantize_e<E>(kv[j], inv_k, kv[j]);
             vq = quantize_e<E>(vv[j], inv_v, vv[j]);
         }
-        float s = 0.f;
+        if (pos >= pad) {
+            float s = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            s = fmaf(qv[e], kv[j][e], s);
-        }
-        s = group_sum<64>(s) * score_log2;
-        const float m2 = fmaxf(mx, s);
-        const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
-        const float w = fast_exp2(s - m2);
-        den = den * a + w;
-        mx = m2;
+            for (int e = 0; e < E; ++e) {
+                s = fmaf(qv[e], kv[j][e], s);
+            }
+            s = group_sum<64>(s) * score_log2;
+            const float m2 = fmaxf(mx, s);
+            const float a = mx == kNegInf ? 0.f : fast_exp2(mx - m2);
+            const float w = fast_exp2(s - m2);
+            den = den * a + w;
+            mx = m2;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            acc[e] = fmaf(w, vv[j][e] * v_mul, acc[e] * a);
+            for (int e = 0; e < E; ++e) {
+                acc[e] = fmaf(w, vv[j][e] * v_mul, acc[e] * a);
+            }
         }
         if (i == j && h == kvh * p.group) {
             const int32_t page = f.block_table[static_cast<int64_t>(t.b) * f.bt_stride + (pos >> p.page_shift)];

@@ -114,6 +114,7 @@ struct FoldParams {
     int32_t kv_fp8;
     const float* k_scale; // FP8 caches: per-KV-head scales, or null (1)
     const float* v_scale;
+    const int32_t* kv_start; // optional [B] (cache_leftpad): a new token below it is stored, not attended
 };
 
 // Query rows per wave of the tile schedule's stream combine.

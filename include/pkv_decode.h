@@ -292,7 +292,7 @@ size_t pkv_decode_append_workspace_size(const pkv_decode_desc* desc, int num_spl
  * kernel first and then attends the longer rows (three kernels), -1 if desc
  * is invalid.  Folded: as many new tokens as query tokens, at most 8 (the
  * decode step and the speculative verify step, causal or not), 16-bit or
- * FP8 caches, no window, ALiBi, softcap, cache_leftpad or rotary tables, the tile schedule
+ * FP8 caches, no window, ALiBi, softcap or rotary tables, the tile schedule
  * with its row-per-wave combine.  The outputs agree within the decode
  * tolerances (the new tokens' scores are summed in a different order); the
  * caches are written identically.  No

@@ -482,12 +482,12 @@ def test_softcap_needs_the_mfma_path_and_takes_the_masked_policy():
     assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(softcap=30.0)), 0, 1) == 0
 
 
-def test_cache_leftpad_needs_alignment_and_the_mfma_path_and_never_folds():
+def test_cache_leftpad_needs_alignment_and_the_mfma_path_and_folds():
     assert pagedkv.workspace_size(base_desc(cache_leftpad=4096 + 2), 0) == 0  # not 4-byte aligned
     assert pagedkv.workspace_size(base_desc(cache_leftpad=4096), 0) > 0
     assert pagedkv.workspace_size(base_desc(cache_leftpad=4096, path=pagedkv.PKV_PATH_VALU), 0) == 0
     lib = _lib.load()
-    assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(cache_leftpad=4096)), 0, 1) == 0
+    assert lib.pkv_decode_append_folds(ctypes.byref(base_desc(cache_leftpad=4096)), 0, 1) == 1
     assert lib.pkv_decode_path(ctypes.byref(base_desc(cache_leftpad=4096))) == pagedkv.PKV_PATH_MFMA
 
 

@@ -77,8 +77,8 @@ def test_captured_append_and_decode_replay_like_eager(rng, splits):
 @pytest.mark.parametrize("fp8,leftpad", [(False, False), (True, False), (False, True)])
 def test_captured_verify_step_with_lse_replays_like_eager(rng, fp8, leftpad):
     """The speculative verify step (4 new tokens, 4 causal queries) with softmax_lse, captured:
-    the folded append on 16-bit and FP8 caches, and with a cache_leftpad the append kernel in
-    front of a masked decode.  Every replay after eager work equals the eager call bit for bit:
+    the folded append on 16-bit and FP8 caches, and with a cache_leftpad (the partition then
+    masked).  Every replay after eager work equals the eager call bit for bit:
     output, LSE and caches."""
     import pagedkv
 
@@ -110,7 +110,7 @@ def test_captured_verify_step_with_lse_replays_like_eager(rng, fp8, leftpad):
                              cache_leftpad=lp.data_ptr() if leftpad else 0)
     lib = pagedkv._lib.load()
     import ctypes
-    assert lib.pkv_decode_append_folds(ctypes.byref(desc), 0, n) == (0 if leftpad else 1)
+    assert lib.pkv_decode_append_folds(ctypes.byref(desc), 0, n) == 1
     ws = torch.empty(max(int(lib.pkv_decode_append_workspace_size(ctypes.byref(desc), 0, n)), 256),
                      dtype=torch.uint8, device="cuda")
 

@@ -184,3 +184,59 @@ def test_full_size_config_with_leftpad_and_softcap(name):
                                  cfg.seqlens, cfg.scale, dt, lse=True, softcap=30.0, leftpad=lp)
     assert_close(out, want, dt)
     assert_lse(lse, want_lse)
+
+
+@pytest.mark.parametrize("M,causal,fp8", [(1, False, False), (1, False, True), (4, True, False), (3, False, True)])
+def test_leftpad_with_the_folded_append(M, causal, fp8):
+    """decode_append with as many new tokens as query tokens on a tile-schedule shape, where the
+    append folds into the combine: the partition masks the padded cached keys, the combine skips
+    new tokens below the leftpad (rows padded past their cached end) but still stores them."""
+    import ctypes
+
+    import pagedkv
+
+    torch = torch_mod()
+    announce("leftpad-fold", M, causal, fp8)
+    rng = np.random.default_rng(7800 + M + 10 * int(fp8))
+    B, H, Hk, D, P, dtype = 16, 32, 8, 128, 16, 1
+    lens = rng.integers(200, 900, B).astype(np.int32)
+    lp = np.minimum(rng.integers(0, 300, B), lens).astype(np.int32)
+    lp[0] = lens[0] + 1        # the first new token of row 0 is padding too
+    lp[1] = lens[1] + M + 5    # every key of row 1, new ones included
+    lp[2] = lens[2]            # every cached key of row 2
+    _, k16, v16, bt, _ = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=lens + M, dtype=dtype)
+    q = rand_bits(rng, (B, M, H, D), dtype)
+    nk = rand_bits(rng, (B, M, Hk, D), dtype)
+    nv = rand_bits(rng, (B, M, Hk, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=k16.shape[0],
+                             block_table_stride=bt.shape[1], dtype=dtype, seqlen_q=M, causal=causal,
+                             kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
+                             cache_leftpad=4096)
+    assert pagedkv._lib.load().pkv_decode_append_folds(ctypes.byref(desc), 0, M) == 1
+    ks = vs = None
+    if fp8:
+        ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        kc, vc = fp8_cache(rng, k16.shape, ks), fp8_cache(rng, k16.shape, vs)
+        want_k, want_v = po.append_kv(kc, vc, bt, lens, po.quantize_e4m3(nk, dtype, ks),
+                                      po.quantize_e4m3(nv, dtype, vs))
+        want, want_lse = po.attn8_f64(q, want_k, want_v, bt, po.appended_seqlens(lens, M), scale, dtype, k_scale=ks,
+                                      v_scale=vs, causal=causal, lse=True, leftpad=lp)
+        kd, vd = to_dev8(kc), to_dev8(vc)
+    else:
+        kc, vc = k16, v16
+        want_k, want_v = po.append_kv(kc, vc, bt, lens, nk, nv)
+        want, want_lse = po.attn_f64(q, want_k, want_v, bt, po.appended_seqlens(lens, M), scale, dtype,
+                                     causal=causal, lse=True, leftpad=lp)
+        kd, vd = to_dev(kc, dtype), to_dev(vc, dtype)
+    lse = lse_buffer(B, H, M)
+    out = pagedkv.decode(to_dev(q, dtype), kd, vd, i32(bt), i32(lens), scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype), causal=causal, k_scale=f32(ks), v_scale=f32(vs), softmax_lse=lse,
+                         cache_leftpad=i32(lp))
+    torch.cuda.synchronize()
+    from test_gpu_fp8 import from_dev8
+    np.testing.assert_array_equal(from_dev8(kd) if fp8 else from_dev(kd), want_k)
+    np.testing.assert_array_equal(from_dev8(vd) if fp8 else from_dev(vd), want_v)
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
