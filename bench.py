@@ -349,6 +349,8 @@ def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dic
             s_["v_scale"] = torch.rand(cfg.num_heads_k, device=dev) + 0.5
         if M > 1:
             s_["q"] = torch.randn((cfg.batch, M, cfg.num_heads, cfg.head_dim), device=dev).to(s_["q"].dtype)
+        if args.leftpad > 0:
+            s_["leftpad"] = torch.clamp(s_["cache_seqlens"], max=args.leftpad).to(torch.int32).contiguous()
     sh = torch.cuda.current_stream(dev).cuda_stream
     base = sets[0]
     desc = pagedkv.make_desc(
@@ -358,6 +360,7 @@ def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dic
         max_seqlen=int(cfg.seqlens.max()) - M, path=args.path, seqlen_q=M, causal=args.causal,
         kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
         k_scale=base["k_scale"].data_ptr() if fp8 else 0, v_scale=base["v_scale"].data_ptr() if fp8 else 0,
+        cache_leftpad=base["leftpad"].data_ptr() if args.leftpad > 0 else 0,
     )
     splits_req = args.splits if args.splits is not None else cfg.num_splits
     lib = pagedkv._lib.load()
@@ -375,6 +378,8 @@ def run_decode_append(name: str, args, torch, pagedkv, events: HipEvents) -> dic
         s, (kn, vn), sl, o = sets[i % len(sets)], news[i % len(sets)], prev[i % len(sets)], outs[i % len(sets)]
         if fp8:
             desc.k_scale, desc.v_scale = s["k_scale"].data_ptr(), s["v_scale"].data_ptr()
+        if args.leftpad > 0:
+            desc.cache_leftpad = s["leftpad"].data_ptr()
         st = lib.pkv_decode_append(s["q"].data_ptr(), kn.data_ptr(), vn.data_ptr(), s["k_cache"].data_ptr(),
                                    s["v_cache"].data_ptr(), s["block_table"].data_ptr(), sl.data_ptr(), M,
                                    float(cfg.scale), splits_req, o.data_ptr(), ctypes.byref(desc), sh)
@@ -484,7 +489,8 @@ def main() -> int:
     ap.add_argument("--window", type=int, nargs=2, default=(-1, -1), metavar=("LEFT", "RIGHT"),
                     help="sliding window (decode op); -1 = unbounded")
     ap.add_argument("--leftpad", type=int, default=0,
-                    help="cache_leftpad (decode op): the first N keys of every row are padding (read and masked)")
+                    help="cache_leftpad (decode and decode_append ops): the first N keys of every row are padding "
+                         "(read and masked)")
     ap.add_argument("--softcap", type=float, default=0.0,
                     help="score softcap (decode op): softcap * tanh(s / softcap), flash-attn's softcap")
     ap.add_argument("--kv", choices=("same", "fp8"), default="same",
@@ -612,10 +618,11 @@ def run_op(args, torch, pagedkv, events: HipEvents) -> int:
                 "dtype": cfg.dtype,
                 "config": {**cfg.describe(), "workload": "decode_append", "seqlen_new": M, "seqlen_q": M,
                            "causal": args.causal, "folded": res["folded"],
-                           **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {})},
+                           **({"kv_dtype": "fp8_e4m3"} if args.kv == "fp8" else {}),
+                           **({"cache_leftpad": args.leftpad} if args.leftpad > 0 else {})},
                 "us_per_call": round(res["ms"] * 1e3, 2), "cpu_baseline": None}
         print(f"[bench] decode_append {cfg.name} M={M}{' causal' if args.causal else ''} kv={args.kv} "
-              f"folded={res['folded']}: {res['ms'] * 1e3:.2f} us/call, {res['kv_gbps']:.1f} GB/s KV",
+              f"{f'leftpad={args.leftpad} ' if args.leftpad > 0 else ''}folded={res['folded']}: {res['ms'] * 1e3:.2f} us/call, {res['kv_gbps']:.1f} GB/s KV",
               file=sys.stderr, flush=True)
     if args.json_out:
         with open(args.json_out, "a") as f:
