@@ -24,7 +24,7 @@ constexpr int kComputeUnits = pkv::kComputeUnits;
 
 // Tile-balanced schedule: one workgroup of pkv::kTileWaves waves per CU.  A
 // call fills the chip when it has kFillTilesPerWorker 16-token tiles per wave
-// for every wave; smaller calls get no fewer than PKV_MIN_TILES_PER_WORKER
+// for every wave; smaller calls get no fewer than kMinTilesPerWorker
 // tiles per wave (each wave's share starts with a few dependent loads that
 // more tiles amortise, but on a chip the call does not fill, fewer tiles per
 // wave shorten the chain).  Measured on MI355X, 8 -> 2 tiles: the evaluator's
@@ -32,10 +32,7 @@ constexpr int kComputeUnits = pkv::kComputeUnits;
 // 15.4-22.5 -> 12.7-20.7 µs, its 8192-token single row 16.6 -> 14.3 µs; calls
 // that fill the chip (C2-C5) unchanged.
 constexpr int64_t kFillTilesPerWorker = 8;
-#ifndef PKV_MIN_TILES_PER_WORKER
-#define PKV_MIN_TILES_PER_WORKER 2
-#endif
-constexpr int64_t kMinTilesPerWorker = PKV_MIN_TILES_PER_WORKER;
+constexpr int64_t kMinTilesPerWorker = 2;
 
 struct Resolved {
     int64_t B, H, Hk, D, P, group;
@@ -206,13 +203,11 @@ int64_t part_heads(const Resolved& r) { return std::min<int64_t>(r.rows, r.heads
 
 // Gang of the tile-balanced schedule: 2^s waves of a workgroup share one unit
 // share and stream adjacent streams of it, so a CU reads 2^s adjacent head
-// rows of each token row together.  The largest 2^s <= 2^PKV_GANG_SHIFT_MAX
+// rows of each token row together.  The largest 2^s <= 2^kGangShiftMax
 // dividing both the streams per row and the workgroup's waves.
-#ifndef PKV_GANG_SHIFT_MAX
-#define PKV_GANG_SHIFT_MAX 2
-#endif
+constexpr int kGangShiftMax = 2;
 int gang_shift(const Resolved& r) {
-    int s = PKV_GANG_SHIFT_MAX;
+    int s = kGangShiftMax;
     while (s > 0 && (streams_per_row(r) % (int64_t{1} << s) != 0 || pkv::kTileWaves % (1 << s) != 0)) {
         --s;
     }

@@ -410,10 +410,7 @@ constexpr int kComputeUnits = 256;
 // Waves per workgroup (= per CU) of the tile-balanced partition kernel.
 // Measured on MI355X over the five workload shapes: 4 (one per SIMD) streams
 // faster than 2, 3, 5, 6 or 8, and than 4 with two tiles of prefetch per wave.
-#ifndef PKV_TILE_WAVES
-#define PKV_TILE_WAVES 4
-#endif
-constexpr int kTileWaves = PKV_TILE_WAVES;
+constexpr int kTileWaves = 4;
 
 __device__ __forceinline__ int32_t wave_item() {
     return static_cast<int32_t>(blockIdx.x) * kWavesPerGroup + static_cast<int32_t>(threadIdx.x >> 6);
@@ -525,10 +522,7 @@ __device__ __forceinline__ int32_t row_tiles(const int32_t* __restrict__ seqlens
 // inside its share is charged for them, so workers with an extra segment do
 // not end up last.  The header units precede the stream's tiles and are never
 // processed.
-#ifndef PKV_HEADER_TILES
-#define PKV_HEADER_TILES 2
-#endif
-constexpr int32_t kHeaderTiles = PKV_HEADER_TILES;
+constexpr int32_t kHeaderTiles = 2;
 
 __device__ __forceinline__ int32_t stream_units(int32_t n) { return n > 0 ? n + kHeaderTiles : 0; }
 

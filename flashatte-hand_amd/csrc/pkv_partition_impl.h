@@ -77,12 +77,6 @@ __device__ __forceinline__ f32x4 mfma_16x16x16(const uint2& a, const uint2& b, f
     }
 }
 
-// PV form: 0 = one 16x16x32 MFMA per output tile over (token, head /
-// remainder) pairs, 1 = two 16x16x16 MFMAs (heads, then remainders).
-#ifndef PKV_PV_TWO_MFMA
-#define PKV_PV_TWO_MFMA 0
-#endif
-
 // Cache element width: 2 bytes (fp16 / bf16, the compute dtype) or 1 byte
 // (OCP FP8 e4m3, converted to the compute dtype when staged).  Either way a
 // lane takes 8 elements of a token row (16 or 8 bytes), so the staged LDS
@@ -305,6 +299,7 @@ struct MfmaMath {
         float slope[NB];
         int32_t all_lo; // max over the slice's rows of lo
         int32_t all_hi; // min over the slice's rows of hi
+        int32_t pad;    // cache_leftpad of the row (wave-uniform; 0 without one)
         bool alibi;
         float cap;      // softcap in log2 units (0 = none) and its reciprocal
         float inv_cap;
@@ -394,9 +389,32 @@ struct MfmaMath {
             }
             q.all_lo = uniform(all_lo);
             q.all_hi = uniform(all_hi);
+            q.pad = uniform(pad);
             q.alibi = p.alibi != nullptr;
             q.cap = p.softcap_log2;
             q.inv_cap = p.softcap_log2 > 0.f ? 1.f / p.softcap_log2 : 0.f;
+        }
+    }
+
+    // cache_leftpad: zero the staged V rows of the tile's tokens below the
+    // row's pad.  Their probabilities are 0, but 0 times a NaN or an infinity
+    // (whatever the pad region holds: stale memory, FP8 bytes 0x7f / 0xff)
+    // would still poison the PV product.  Rows past the range's end hold
+    // copies of token end - 1 (load_tile clamps them there), so when that
+    // token is padding too the whole tile is cleared.  Masked K rows need
+    // nothing: their scores are replaced by -inf before use.
+    __device__ static void clear_pad_rows(const Q& q, uint16_t* lds, int t0, int end, int lane) {
+        if constexpr (MQ) {
+            if (t0 < q.pad) {
+                constexpr int CH = D / 8; // 16-byte chunks per row
+                const int rows = q.pad >= end ? 16 : min(q.pad - t0, 16);
+                uint16_t* vt = lds + VTile<D>::kElems;
+                for (int idx = lane; idx < rows * CH; idx += 64) {
+                    const int r = idx / CH;
+                    *reinterpret_cast<uint4*>(vt + r * VTile<D>::kRow + 8 * (idx - r * CH)) =
+                        make_uint4(0u, 0u, 0u, 0u);
+                }
+            }
         }
     }
 
@@ -542,23 +560,10 @@ struct MfmaMath {
             }
             return;
         }
-#if PKV_PV_TWO_MFMA
-        // Two 16x16x16 MFMAs per output tile, against the heads and then the
-        // remainders (all heads first, so no MFMA waits on the one before).
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = mfma_16x16x16<BF16>(av[dt], make_uint2(pb[nb].x, pb[nb].y), a.o[nb][dt]);
-            }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                a.o[nb][dt] = mfma_16x16x16<BF16>(av[dt], make_uint2(pb[nb].z, pb[nb].w), a.o[nb][dt]);
-            }
-        }
-#else
         // 16x16x32 MFMA over (token, part) pairs: A holds each token's V^T
         // column twice (once against the head, once against the remainder).
+        // (Two 16x16x16 MFMAs per output tile, heads then remainders, measured
+        // no faster.)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -567,7 +572,6 @@ struct MfmaMath {
                 a.o[nb][dt] = mfma_16x16x32<BF16>(a2, pb[nb], a.o[nb][dt]);
             }
         }
-#endif
     }
 
     // l holds this lane's 4-token partial sums; total over the 4 lanes of row n.
@@ -745,6 +749,7 @@ struct ValuMath {
     }
 
     __device__ static void set_mask(const PartitionParams&, int, int, int, int, Q&) {}
+    __device__ static void clear_pad_rows(const Q&, uint16_t*, int, int, int) {}
 
     __device__ static void init(Acc& a) {
 #pragma unroll
@@ -956,6 +961,7 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
             stage_tile<D, FP8, Math::kBF16>(r[d], lds, lane);
+            Math::clear_pad_rows(q, lds, t, end, lane);
             // The whole tile is staged before the prefetch goes out.  Left to
             // itself the scheduler may interleave the two (issue part of the
             // prefetch after the first chunks land): FP8 C2 measured 28.7
@@ -973,6 +979,7 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
     for (int d = 0; d + 1 < DEPTH; ++d) {
         if (k + d < ntiles) {
             stage_tile<D, FP8, Math::kBF16>(r[d], lds, lane);
+            Math::clear_pad_rows(q, lds, t, end, lane);
             Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
         }
@@ -1293,21 +1300,17 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
 // Tiles of K/V loads in flight per wave.  The tile-balanced schedule keeps the
 // whole chip busy and streams fastest with one; split schedules with fewer
 // items than CUs are latency-bound and take two.
-#ifndef PKV_MFMA_DEPTH
-#define PKV_MFMA_DEPTH 1
-#endif
+constexpr int kMfmaDepth = 1;
 constexpr int kSplitDepthFewItems = 2;
 
 // FP8 tiles are half the bytes: two of them in flight keep as many bytes
 // loading as one 16-bit tile.  Measured on MI355X (C2 / C3 / C4 / C5 with FP8
 // caches): 40.1 / 164 / 187 / 112 us with one tile, 32.6 / 129 / 134 / 111 us
 // with two; eight waves per CU instead of four gave 32.9 / 132 / 140 / 118.
-#ifndef PKV_FP8_DEPTH
-#define PKV_FP8_DEPTH 2
-#endif
+constexpr int kFp8Depth = 2;
 template <bool FP8>
 constexpr int kv_depth() {
-    return FP8 ? PKV_FP8_DEPTH : PKV_MFMA_DEPTH;
+    return FP8 ? kFp8Depth : kMfmaDepth;
 }
 
 template <typename Math, int D, bool WIDE, bool FP8>

@@ -302,8 +302,9 @@ def decode(
     lse_ptr = 0
     if softmax_lse is not None:
         _check_cuda("softmax_lse", softmax_lse)
-        if softmax_lse.dtype != torch.float32 or tuple(softmax_lse.shape) != (B, H, M):
-            raise PkvError(PKV_EINVAL, "softmax_lse must be fp32 [B, H, M]")
+        if softmax_lse.dtype != torch.float32 or tuple(softmax_lse.shape) != (B, H, M) or \
+                not softmax_lse.is_contiguous():
+            raise PkvError(PKV_EINVAL, "softmax_lse must be a contiguous fp32 [B, H, M] tensor")
         lse_ptr = softmax_lse.data_ptr()
     leftpad_ptr = 0
     if cache_leftpad is not None:
@@ -484,7 +485,11 @@ def _contiguous_as_pages(q, k_cache, v_cache, cache_batch_idx):
         table = _IDENTITY_TABLES.get(key)
         if table is None:
             table = torch.arange(B * per_row, dtype=torch.int32, device=q.device).view(B, per_row)
-            if len(_IDENTITY_TABLES) < 64:
+            # Kept only when built eagerly and finished: a table made under graph capture is a
+            # graph node of the capture's private pool (unfilled until replayed), and one still
+            # being filled on this stream must not be read from another stream.
+            if len(_IDENTITY_TABLES) < 64 and not torch.cuda.is_current_stream_capturing():
+                torch.cuda.current_stream(q.device).synchronize()
                 _IDENTITY_TABLES[key] = table
         return (k_cache.view(b_cache * per_row, P, Hk, D), v_cache.view(b_cache * per_row, P, Hk, D), table)
     else:

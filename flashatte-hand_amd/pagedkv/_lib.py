@@ -6,11 +6,10 @@ built raises, so no caller can silently fall back to another implementation.
 from __future__ import annotations
 
 import ctypes
-import os
 from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent.parent
-LIB_PATH = Path(os.environ.get("PKV_DECODE_LIB", PKG_ROOT / "lib" / "libpkv_decode.so"))
+LIB_PATH = PKG_ROOT / "lib" / "libpkv_decode.so"
 
 PKV_OK = 0
 PKV_EINVAL = 1

@@ -63,22 +63,18 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(out, flush=True)
 
 
-def build_library(verbose: bool = False, jobs: int = 0, out: Path | None = None,
-                  defines: tuple[str, ...] = ()) -> Path:
-    """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds).
-
-    `out` / `defines` build a variant elsewhere (tuning experiments)."""
+def build_library(verbose: bool = False, jobs: int = 0) -> Path:
+    """Compile every HIP source for gfx950 and link libpkv_decode.so (always rebuilds)."""
     hipcc = _hipcc()
-    lib_path = Path(out) if out else LIB_PATH
-    build_dir = BUILD_DIR if out is None else lib_path.parent / "_build"
+    lib_path = LIB_PATH
+    build_dir = BUILD_DIR
     build_dir.mkdir(parents=True, exist_ok=True)
     lib_path.parent.mkdir(parents=True, exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
         obj = build_dir / (src.rsplit(".", 1)[0] + ".o")
-        lang = ["-x", "hip"]
-        cmds.append([hipcc, *HIPCC_FLAGS, *[f"-D{d}" for d in defines], *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        cmds.append([hipcc, *HIPCC_FLAGS, "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
     if jobs <= 0:
         jobs = min(len(cmds), max(1, min(16, os.cpu_count() or 1)))

@@ -184,8 +184,7 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits);
 /*
  * pkv_decode for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation).  No counterpart in
- * the reference, whose run_kernel grows a hidden device workspace on demand.
- * Same arguments and results as pkv_decode, but the split partials go to a
+ * the reference.  Same arguments and results as pkv_decode, but the split partials go to a
  * scratch buffer of PKV_SCRATCH_BYTES in device memory that the library holds
  * on each GPU for the life of the process (a static device array);
  * desc->workspace and desc->workspace_bytes are ignored.  The call allocates

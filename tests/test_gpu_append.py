@@ -338,6 +338,8 @@ FOLD_MULTI = [
     (12, 32, 8, 128, 64, [511, 0, 64, 63], 300, 1, False, 1, True),    # FP8 decode step
     (12, 32, 8, 128, 16, [0, 15, 16, 100], 400, 4, True, 0, True),     # FP8 verify
     (12, 16, 4, 256, 16, [33, 0], 300, 2, True, 1, True),              # FP8, head_dim 256
+    (12, 8, 8, 64, 16, [17, 0, 300], 600, 1, False, 0, True),          # FP8 decode step, head_dim 64
+    (12, 16, 4, 64, 16, [33, 0, 15], 300, 3, True, 1, True),           # FP8 verify, head_dim 64
 ]
 
 
@@ -387,5 +389,48 @@ def test_decode_append_folded_verify_and_fp8(case):
     else:
         np.testing.assert_array_equal(from_dev(dk), want_k)
         np.testing.assert_array_equal(from_dev(dv), want_v)
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_decode_append_folded_fp8_multi_at_row_capacity(rng, D):
+    """FP8 caches, three causal drafts per row, rows filled to the block table's capacity (24
+    pages of 16 = 384 tokens): 381 cached tokens take the drafts in the last three slots, 380
+    and 378 end just short of it, 0 starts a row.  Caches bit for bit and the output and LSE
+    against the oracle."""
+    import pagedkv
+    from test_gpu_fp8 import assert_close, f32, fp8_cache, from_dev8, to_dev8
+    from test_gpu_lse import assert_lse, lse_buffer
+
+    torch = torch_mod()
+    announce("decode_append-folded-fp8-capacity", D)
+    B, H, Hk, P, n, dtype = 12, 32, 8, 16, 3, 1
+    stride = 24
+    pool = B * stride + 2
+    bt = rng.permutation(pool).astype(np.int32)[:B * stride].reshape(B, stride).copy()
+    sl = np.array(fold_lens([381, 380, 378, 0], 200, B), dtype=np.int32)
+    q = rand_bits(rng, (B, n, H, D), dtype)
+    nk = rand_bits(rng, (B, n, Hk, D), dtype)
+    nv = rand_bits(rng, (B, n, Hk, D), dtype)
+    ks = rng.uniform(0.05, 0.5, Hk).astype(np.float32)
+    vs = rng.uniform(0.05, 0.5, Hk).astype(np.float32)
+    kc = fp8_cache(rng, (pool, P, Hk, D), ks)
+    vc = fp8_cache(rng, (pool, P, Hk, D), vs)
+    desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=pool,
+                             block_table_stride=stride, seqlen_q=n, causal=True, dtype=pagedkv.PKV_DTYPE_BF16,
+                             kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3)
+    assert pagedkv.append_folds(desc, 0, n)
+    scale = 1.0 / math.sqrt(D)
+    want_k, want_v = po.append_kv(kc, vc, bt, sl, po.quantize_e4m3(nk, dtype, ks), po.quantize_e4m3(nv, dtype, vs))
+    want, want_lse = po.attn8_f64(q, want_k, want_v, bt, po.appended_seqlens(sl, n), scale, dtype, k_scale=ks,
+                                  v_scale=vs, causal=True, lse=True)
+    dk, dv = to_dev8(kc), to_dev8(vc)
+    lse = lse_buffer(B, H, n)
+    out = pagedkv.decode(to_dev(q, dtype), dk, dv, i32(bt), i32(sl), scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype), causal=True, k_scale=f32(ks), v_scale=f32(vs), softmax_lse=lse)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(from_dev8(dk), want_k)
+    np.testing.assert_array_equal(from_dev8(dv), want_v)
     assert_close(out, want, dtype)
     assert_lse(lse, want_lse)

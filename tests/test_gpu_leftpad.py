@@ -7,8 +7,8 @@ tolerances, softmax_lse as in tests/test_gpu_lse.py.
 A leftpad sends the call to the masked MFMA policy.  Cases: one query token without other
 masks (tile schedule, single pass, page splits), rows whose padding covers every key
 (zeros, LSE +inf), the speculative verify with a causal mask, a window with ALiBi,
-head_dim 256, FP8 caches, many rows on the tile schedule, and flash-attn's contiguous
-caches with appended (and rotated) tokens.
+head_dim 256, FP8 caches, many rows on the tile schedule, flash-attn's contiguous
+caches with appended (and rotated) tokens, and a pad region holding NaN and infinities.
 """
 from __future__ import annotations
 
@@ -236,6 +236,129 @@ def test_leftpad_with_the_folded_append(M, causal, fp8):
                          cache_leftpad=i32(lp))
     torch.cuda.synchronize()
     from test_gpu_fp8 import from_dev8
+    np.testing.assert_array_equal(from_dev8(kd) if fp8 else from_dev(kd), want_k)
+    np.testing.assert_array_equal(from_dev8(vd) if fp8 else from_dev(vd), want_v)
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
+
+
+def _poison_below_pad(cache, bt, lp, P, bits):
+    """Writes `bits` over every element of the tokens below each row's leftpad: the region
+    flash-attn never reads."""
+    for b in range(len(lp)):
+        for t in range(int(lp[b])):
+            page = bt[b, t // P]
+            if page >= 0:
+                cache[page, t % P] = bits
+
+
+# (B, H, Hk, D, P, seqlens, leftpad, M, causal, dtype, fp8): pads inside a tile, on a tile
+# boundary, covering whole tiles and pages, and covering the whole row.
+NAN_CASES = [
+    (4, 32, 8, 128, 16, [700, 40, 1, 300], [100, 40, 0, 299], 1, False, 1, False),
+    (3, 16, 4, 256, 64, [900, 33, 2049], [450, 1, 1040], 1, False, 0, False),
+    (3, 32, 8, 128, 64, [1000, 5, 2049], [63, 6, 1024], 4, True, 1, False),
+    (3, 16, 4, 128, 16, [500, 33, 97], [250, 33, 16], 1, False, 1, True),
+    (2, 16, 2, 64, 16, [300, 260], [17, 200], 2, True, 0, True),
+]
+
+
+@pytest.mark.parametrize("splits", [0, 1, 3])
+@pytest.mark.parametrize("case", range(len(NAN_CASES)))
+def test_leftpad_region_holding_nan_and_inf(splits, case):
+    """Every K / V element below each row's leftpad is NaN (K) or NaN / infinity (V); 16-bit
+    NaN 0x7fc0 / 0x7e00 and infinity, FP8 0x7f / 0xff.  flash-attn never reads that region, so
+    the output and LSE must match the oracle, which skips it, on every schedule (tile schedule
+    with its combine, single pass, page splits)."""
+    import pagedkv
+
+    torch = torch_mod()
+    B, H, Hk, D, P, seqlens, leftpad, M, causal, dtype, fp8 = NAN_CASES[case]
+    announce("leftpad-nan", NAN_CASES[case], "splits", splits)
+    rng = np.random.default_rng(7500 + case)
+    _, k16, v16, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=seqlens, dtype=dtype)
+    lp = np.asarray(leftpad, np.int32)
+    q = rand_bits(rng, (B, M, H, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    ks = vs = None
+    if fp8:
+        ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        kc, vc = fp8_cache(rng, k16.shape, ks), fp8_cache(rng, k16.shape, vs)
+        _poison_below_pad(kc, bt, lp, P, 0x7F)
+        _poison_below_pad(vc, bt, lp, P, 0xFF if case % 2 else 0x7F)
+        want, want_lse = po.attn8_f64(q, kc, vc, bt, sl, scale, dtype, k_scale=ks, v_scale=vs, causal=causal,
+                                      lse=True, leftpad=lp)
+        kd, vd = to_dev8(kc), to_dev8(vc)
+    else:
+        nan = 0x7FC0 if dtype == 1 else 0x7E00
+        inf = 0x7F80 if dtype == 1 else 0x7C00
+        _poison_below_pad(k16, bt, lp, P, nan)
+        _poison_below_pad(v16, bt, lp, P, inf if case % 2 else nan)
+        want, want_lse = po.attn_f64(q, k16, v16, bt, sl, scale, dtype, causal=causal, lse=True, leftpad=lp)
+        kd, vd = to_dev(k16, dtype), to_dev(v16, dtype)
+    assert np.all(np.isfinite(want))
+    lse = lse_buffer(B, H, M)
+    out = pagedkv.decode(to_dev(q, dtype), kd, vd, i32(bt), i32(sl), scale, splits, causal=causal,
+                         k_scale=f32(ks), v_scale=f32(vs), softmax_lse=lse, cache_leftpad=i32(lp))
+    torch.cuda.synchronize()
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
+
+
+@pytest.mark.parametrize("M,fp8", [(1, False), (2, True)])
+def test_leftpad_region_holding_nan_with_the_folded_append(M, fp8):
+    """The folded decode_append (the partition over the cached keys, the combine adding and
+    storing the new ones) with NaN below every row's leftpad: outputs and caches as the
+    oracle gives them."""
+    import ctypes
+
+    import pagedkv
+    from test_gpu_fp8 import from_dev8
+
+    torch = torch_mod()
+    announce("leftpad-nan-fold", M, fp8)
+    rng = np.random.default_rng(7600 + M)
+    B, H, Hk, D, P, dtype = 16, 32, 8, 128, 16, 1
+    lens = rng.integers(200, 900, B).astype(np.int32)
+    lp = np.minimum(rng.integers(0, 300, B), lens).astype(np.int32)
+    lp[2] = lens[2]
+    _, k16, v16, bt, _ = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=lens + M, dtype=dtype)
+    q = rand_bits(rng, (B, M, H, D), dtype)
+    nk = rand_bits(rng, (B, M, Hk, D), dtype)
+    nv = rand_bits(rng, (B, M, Hk, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=k16.shape[0],
+                             block_table_stride=bt.shape[1], dtype=dtype, seqlen_q=M,
+                             kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3 if fp8 else pagedkv.PKV_KV_DTYPE_SAME,
+                             cache_leftpad=4096)
+    assert pagedkv._lib.load().pkv_decode_append_folds(ctypes.byref(desc), 0, M) == 1
+    ks = vs = None
+    if fp8:
+        ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32)
+        kc, vc = fp8_cache(rng, k16.shape, ks), fp8_cache(rng, k16.shape, vs)
+        _poison_below_pad(kc, bt, lp, P, 0x7F)
+        _poison_below_pad(vc, bt, lp, P, 0xFF)
+        want_k, want_v = po.append_kv(kc, vc, bt, lens, po.quantize_e4m3(nk, dtype, ks),
+                                      po.quantize_e4m3(nv, dtype, vs))
+        want, want_lse = po.attn8_f64(q, want_k, want_v, bt, po.appended_seqlens(lens, M), scale, dtype, k_scale=ks,
+                                      v_scale=vs, lse=True, leftpad=lp)
+        kd, vd = to_dev8(kc), to_dev8(vc)
+    else:
+        kc, vc = k16, v16
+        _poison_below_pad(kc, bt, lp, P, 0x7FC0)
+        _poison_below_pad(vc, bt, lp, P, 0x7F80)
+        want_k, want_v = po.append_kv(kc, vc, bt, lens, nk, nv)
+        want, want_lse = po.attn_f64(q, want_k, want_v, bt, po.appended_seqlens(lens, M), scale, dtype, lse=True,
+                                     leftpad=lp)
+        kd, vd = to_dev(kc, dtype), to_dev(vc, dtype)
+    assert np.all(np.isfinite(want))
+    lse = lse_buffer(B, H, M)
+    out = pagedkv.decode(to_dev(q, dtype), kd, vd, i32(bt), i32(lens), scale, 0, k_new=to_dev(nk, dtype),
+                         v_new=to_dev(nv, dtype), k_scale=f32(ks), v_scale=f32(vs), softmax_lse=lse,
+                         cache_leftpad=i32(lp))
+    torch.cuda.synchronize()
     np.testing.assert_array_equal(from_dev8(kd) if fp8 else from_dev(kd), want_k)
     np.testing.assert_array_equal(from_dev8(vd) if fp8 else from_dev(vd), want_v)
     assert_close(out, want, dtype)
