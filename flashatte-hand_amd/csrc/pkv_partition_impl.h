@@ -922,15 +922,24 @@ struct ValuMath {
 
 // ---------------------------------------------------------------- tile pipeline
 
+// Nothing to issue behind a range's first loads.
+struct NoWork {
+    __device__ void operator()() const {}
+};
+
 // Walks the tiles of [t, end) with DEPTH tiles of loads in flight.  RELOAD
 // adds the page-window refresh for ranges longer than 64 pages (a dependent
 // global load, so it drains the pipeline once per 64 pages); the common path
 // has none and every prefetch is unconditional, so all waits are exact.
-template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD, bool FP8>
+// `after` runs once the first DEPTH tiles' loads are out: work that must not
+// hold up the first wait, such as the previous segment's output stores
+// (vmcnt counts stores too, so a store issued before a load delays the wait
+// for that load until the store completes).
+template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD, bool FP8, typename After = NoWork>
 __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_t* __restrict__ bt_row, int last_page,
                                           int& win, int& win_base, const typename Math::Q& q,
                                           typename Math::Acc& acc, uint16_t* lds, int t, int end, int lane,
-                                          int kvh, float scale_log2) {
+                                          int kvh, float scale_log2, After after = {}) {
     auto ensure_window = [&](int tn) {
         if constexpr (RELOAD) {
             const int tl = min(tn + 15, end - 1);
@@ -956,6 +965,7 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
         ensure_window(t + 16 * d);
         load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * d, end, d < ntiles, lane, kvh);
     }
+    after();
     int k = 0;
     for (; k + DEPTH <= ntiles; k += DEPTH) {
 #pragma unroll
@@ -989,10 +999,11 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 // Attention of one head slice over tokens [begin, end) (begin < end), the page
 // window already loaded at some win_base <= begin / P.  Leaves Math's
 // accumulator (unnormalised O, reference max, denominator) finished.
-template <typename Math, int D, bool WIDE, int DEPTH, bool FP8>
+template <typename Math, int D, bool WIDE, int DEPTH, bool FP8, typename After = NoWork>
 __device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
                                              int win_base, const typename Math::Q& q, uint16_t* lds, int begin,
-                                             int end, int lane, int kvh, typename Math::Acc& acc, float scale_log2) {
+                                             int end, int lane, int kvh, typename Math::Acc& acc, float scale_log2,
+                                             After after = {}) {
     Math::init(acc);
     const int last_page = (end - 1) >> p.page_shift;
     // The first tile is loaded without a window check: its page must be one
@@ -1006,10 +1017,10 @@ __device__ __forceinline__ void attend_range(const PartitionParams& p, const int
     if (last_page - win_base < 64) {
         // Common case: the whole range fits in one page window.
         tile_loop<Math, D, WIDE, DEPTH, false, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
-                                                    lane, kvh, scale_log2);
+                                                    lane, kvh, scale_log2, after);
     } else {
         tile_loop<Math, D, WIDE, DEPTH, true, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
-                                                   lane, kvh, scale_log2);
+                                                   lane, kvh, scale_log2, after);
     }
     Math::finish(acc);
 }
@@ -1242,6 +1253,26 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         const int64_t row_first = static_cast<int64_t>(sps) * uniform(rt.before); // first unit of row b
         int u = uniform(static_cast<int32_t>(muldiv(x0 - row_first, 1, units)));  // super-stream of row b
         int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of super-stream (b, u)
+        // A finished segment's rows (output or partial) are stored once the
+        // next segment's first tile loads are out, so their stores do not hold
+        // up that segment's first waits; the last segment's at the end.
+        typename Math::Q pend_q;
+        typename Math::Acc pend_acc;
+        int64_t pend_at = 0; // output row of the slice (final) or partial index of row 0
+        int pend_heads = 0;
+        float pend_scale = 1.f;
+        bool pend_final = false;
+        bool pending = false;
+        auto flush = [&]() {
+            if (pending) {
+                if (pend_final) {
+                    Math::write_final(p, pend_q, pend_at, pend_heads, pend_acc, lane, pend_scale);
+                } else {
+                    Math::write_partial(p, pend_at, 1, pend_heads, pend_acc, lane, pend_scale);
+                }
+                pending = false;
+            }
+        };
         while (true) {
             // The share's tiles of super-stream (b, u): units [x0, x_end) minus the header.
             const int t_lo = static_cast<int>(max(static_cast<int64_t>(0), x0 - vs - kHeaderTiles));
@@ -1266,17 +1297,20 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 const KvScales ks = kv_scales<FP8>(p, kvh);
                 typename Math::Acc acc;
                 attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc,
-                                                        ks.score_log2);
-                if (t_lo == 0 && t_hi == nb && !p.force_partial) {
-                    Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
-                } else {
-                    const int64_t slot =
-                        ((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j;
-                    Math::write_partial(p, slot * p.part_heads, 1, heads_here, acc, lane, ks.out);
-                }
+                                                        ks.score_log2, flush);
+                pend_final = t_lo == 0 && t_hi == nb && !p.force_partial;
+                pend_at = pend_final ? bh_first
+                                     : (((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j) *
+                                           p.part_heads;
+                pend_q = q;
+                pend_acc = acc;
+                pend_heads = heads_here;
+                pend_scale = ks.out;
+                pending = true;
             }
             vs += units;
             if (vs >= x_end) {
+                flush();
                 break;
             }
             // Next super-stream, past rows without tokens (they own no units).

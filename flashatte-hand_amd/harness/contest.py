@@ -6,7 +6,8 @@ bf16, row lengths from the evaluator's formula).  `--set legacy`: the evaluator'
 (eval:339-357: batch 1-128, every row at 512-16384 tokens, 8 query and 8 KV heads, head_dim 256,
 page size 16; 48 shapes); `--set legacy-smoke`: its smoke subset (batch 1-8, 512 / 2048 / 8192
 tokens).  Each case runs as `pkv_harness --case ... --profile contest|legacy --entry run_kernel
---check`: the reference-compatible entry, the harness's own checks, event timing.  Calls rotate
+--check`: the reference-compatible entry, the harness's own checks (every output row against fp64, as
+the evaluator compares the whole tensor, eval:275-276), event timing.  Calls rotate
 over 3 K/V sets unless one call reads more than 2 GB of K/V (no cache holds that; the largest
 legacy pool is 26 GB per cache).  Prints the harness's JSON line per case, then a markdown table;
 exits 1 if any case fails its checks.
@@ -64,9 +65,12 @@ def main(argv=None) -> int:
         print(json.dumps(d), flush=True)
         ok = ok and bool(d["check"]["ok"])
         c = d["case"]
+        ck = d["check"]
         rows.append(f"| {batch} | {seqlen} | {kv_heads} | {c['seqlen_sum']:,} | {SCHEDULES.get(d['schedule'], d['schedule'])}"
-                    f" | {d['us_per_call']:.1f} | {d['kv_gbps']:,.0f} | {'ok' if d['check']['ok'] else 'FAILED'} |")
-    print("\n| B | longest row | Hk | tokens | schedule | µs/call | KV GB/s | checks |\n|--:|--:|--:|--:|---|--:|--:|---|")
+                    f" | {d['us_per_call']:.1f} | {d['kv_gbps']:,.0f} | {ck['sampled_rows']:,} / {ck['rows']:,}"
+                    f" | {ck['max_abs_err']:.2e} | {'ok' if ck['ok'] else 'FAILED'} |")
+    print("\n| B | longest row | Hk | tokens | schedule | µs/call | KV GB/s | rows checked | max abs err | checks |\n"
+          "|--:|--:|--:|--:|---|--:|--:|--:|--:|---|")
     print("\n".join(rows))
     return 0 if ok else 1
 

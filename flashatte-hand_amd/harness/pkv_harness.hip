@@ -4,13 +4,14 @@
 // (make_case, 105-151), run the candidate once and check it (evaluate_case,
 // 199-275), then time repeated calls between two events (time_cuda,
 // 152-165).  flash-attn is not available, so the check is this harness's
-// own: fp64 attention over sampled output rows, bit-exact invariants of the
-// paged layout, and agreement between the two entry points.
+// own: fp64 attention over every output row (the evaluator compares the
+// whole tensor, 275-276), bit-exact invariants of the paged layout, and
+// agreement between the two entry points.
 //
 //   pkv_harness --config c1..c5            the five benchmark workloads
 //   pkv_harness --case B,S,M,H,Hk,D,P      an evaluator case (--profile legacy|contest)
 //   options: --entry pkv_decode|run_kernel  --dtype bf16|f16  --splits N  --causal
-//            --warmup W  --repeat R  --sets N  --seed S  --check
+//            --warmup W  --repeat R  --sets N  --seed S  --check [--check-sample N]
 //
 // Prints one JSON line; exit status 0 = ran (and checks passed), 1 = a check
 // failed, 2 = bad arguments or a HIP / library error.
@@ -26,6 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/pkv_decode.h"
@@ -400,7 +402,8 @@ struct CheckResult {
     bool finite = true;
     int v_copy_rows = 0;
     bool v_copy_exact = true;
-    int sampled = 0;
+    int64_t rows = 0;    // output rows of the call
+    int64_t sampled = 0; // rows checked against fp64 (all of them unless --check-sample)
     double max_abs_err = 0.0;
     double tol = 0.0;
     bool perm_identical = true;
@@ -448,7 +451,7 @@ std::vector<double> attend_row(const Case& c, const std::vector<uint16_t>& q, co
     return o;
 }
 
-CheckResult run_checks(const Case& c, const Runner& run, const KvSet& s, uint64_t seed) {
+CheckResult run_checks(const Case& c, const Runner& run, const KvSet& s, uint64_t seed, int64_t sample) {
     CheckResult r;
     r.tol = c.bf16 ? 1e-2 : 2e-3;
     const size_t out_n = static_cast<size_t>(c.B * c.M * c.H * c.D);
@@ -487,24 +490,50 @@ CheckResult run_checks(const Case& c, const Runner& run, const KvSet& s, uint64_
             }
         }
     }
-    // fp64 attention on sampled rows: row 0, the longest row, and random ones.
+    // fp64 attention on every output row (the reference evaluator compares the
+    // whole tensor, eval:275-276), over the host's threads; with sample > 0,
+    // on row 0, the longest row and sample - 2 random ones instead.
     Rng rng{seed ^ 0x5eedull};
-    std::vector<int64_t> rows = {0};
-    rows.push_back(std::max_element(c.seqlens.begin(), c.seqlens.end()) - c.seqlens.begin());
-    for (int k2 = 0; k2 < 30; ++k2) {
-        rows.push_back(rng.range(0, c.B - 1));
-    }
-    for (int64_t b : rows) {
-        const int64_t i = rng.range(0, c.M - 1);
-        const int64_t h = rng.range(0, c.H - 1);
-        const std::vector<double> want = attend_row(c, q, k, v, b, i, h, run.scale);
-        const uint16_t* got = out.data() + ((b * c.M + i) * c.H + h) * c.D;
-        for (int64_t d = 0; d < c.D; ++d) {
-            r.max_abs_err =
-                std::max(r.max_abs_err, std::fabs(bits_to_double(got[d], c.bf16) - want[static_cast<size_t>(d)]));
+    r.rows = c.B * c.M * c.H;
+    std::vector<int64_t> rows; // flat output rows (b * M + i) * H + h
+    if (sample > 0) {
+        rows.push_back(0);
+        rows.push_back((std::max_element(c.seqlens.begin(), c.seqlens.end()) - c.seqlens.begin()) * c.M * c.H);
+        for (int64_t k2 = 2; k2 < sample; ++k2) {
+            rows.push_back((rng.range(0, c.B - 1) * c.M + rng.range(0, c.M - 1)) * c.H + rng.range(0, c.H - 1));
         }
-        ++r.sampled;
+    } else {
+        rows.resize(static_cast<size_t>(r.rows));
+        for (int64_t x = 0; x < r.rows; ++x) {
+            rows[static_cast<size_t>(x)] = x;
+        }
     }
+    const unsigned threads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<double> worst(threads, 0.0);
+    std::vector<std::thread> pool;
+    for (unsigned w = 0; w < threads; ++w) {
+        pool.emplace_back([&, w]() {
+            for (size_t x = w; x < rows.size(); x += threads) {
+                const int64_t row = rows[x];
+                const int64_t h = row % c.H;
+                const int64_t i = (row / c.H) % c.M;
+                const int64_t b = row / (c.H * c.M);
+                const std::vector<double> want = attend_row(c, q, k, v, b, i, h, run.scale);
+                const uint16_t* got = out.data() + row * c.D;
+                for (int64_t d = 0; d < c.D; ++d) {
+                    worst[w] = std::max(worst[w],
+                                        std::fabs(bits_to_double(got[d], c.bf16) - want[static_cast<size_t>(d)]));
+                }
+            }
+        });
+    }
+    for (std::thread& t : pool) {
+        t.join();
+    }
+    for (double e : worst) {
+        r.max_abs_err = std::max(r.max_abs_err, e);
+    }
+    r.sampled = static_cast<int64_t>(rows.size());
     // Moving every physical page (and block_table with it) changes no bit.
     {
         std::vector<int32_t> perm(static_cast<size_t>(c.num_pages));
@@ -580,7 +609,9 @@ void usage() {
     std::printf(
         "usage: pkv_harness (--config c1..c5 | --case B,S,M,H,Hk,D,P [--profile legacy|contest])\n"
         "                   [--entry pkv_decode|run_kernel] [--dtype bf16|f16] [--splits N] [--causal]\n"
-        "                   [--warmup W] [--repeat R] [--sets N] [--seed S] [--check]\n");
+        "                   [--warmup W] [--repeat R] [--sets N] [--seed S] [--check [--check-sample N]]\n"
+        "  --check: fp64 attention on every output row, V-copy rows, page permutation, both entries;\n"
+        "  --check-sample N: fp64 on N rows only (row 0, the longest row, random ones)\n");
 }
 
 } // namespace
@@ -589,6 +620,7 @@ int main(int argc, char** argv) {
     std::string config, case_spec, profile = "legacy", entry = "pkv_decode", dtype;
     int splits = -1, warmup = 20, repeat = 100, sets = 3;
     bool check = false, causal = false;
+    int64_t check_sample = 0;
     uint64_t seed = 1001;
     for (int a = 1; a < argc; ++a) {
         const std::string arg = argv[a];
@@ -623,6 +655,11 @@ int main(int argc, char** argv) {
             seed = std::strtoull(value().c_str(), nullptr, 10);
         } else if (arg == "--check") {
             check = true;
+        } else if (arg == "--check-sample") {
+            check_sample = std::atoll(value().c_str());
+            if (check_sample < 2) {
+                die("--check-sample takes at least 2 rows");
+            }
         } else if (arg == "--causal") {
             causal = true;
         } else {
@@ -696,7 +733,7 @@ int main(int argc, char** argv) {
 
     CheckResult cr;
     if (check) {
-        cr = run_checks(c, run, kv[0], seed);
+        cr = run_checks(c, run, kv[0], seed, check_sample);
     }
 
     // time_cuda: warm-up calls, then `repeat` calls between two events,
@@ -739,10 +776,11 @@ int main(int argc, char** argv) {
     if (check) {
         std::printf(
             ", \"check\": {\"ok\": %s, \"finite\": %s, \"v_copy_rows\": %d, \"v_copy_exact\": %s, "
-            "\"sampled_rows\": %d, \"max_abs_err\": %.3g, \"tol\": %g, \"permuted_pages_identical\": %s, "
-            "\"entries_identical\": %s}",
+            "\"rows\": %lld, \"sampled_rows\": %lld, \"max_abs_err\": %.3g, \"tol\": %g, "
+            "\"permuted_pages_identical\": %s, \"entries_identical\": %s}",
             cr.ok ? "true" : "false", cr.finite ? "true" : "false", cr.v_copy_rows, cr.v_copy_exact ? "true" : "false",
-            cr.sampled, cr.max_abs_err, cr.tol, cr.perm_identical ? "true" : "false",
+            static_cast<long long>(cr.rows), static_cast<long long>(cr.sampled), cr.max_abs_err, cr.tol,
+            cr.perm_identical ? "true" : "false",
             cr.entries_compared ? (cr.entries_identical ? "true" : "false") : "null");
     }
     std::printf("}\n");
