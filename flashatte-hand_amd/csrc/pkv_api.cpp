@@ -48,6 +48,9 @@ struct Resolved {
     int path;
     int64_t max_pages;
     bool rotary;      // rotary_cos / rotary_sin set (pkv_decode_append only)
+    // KV heads per stream (pkv::PartitionParams::kv_pack).  With 2, Hk, group
+    // and rows count pairs of adjacent KV heads and their query rows.
+    int kv_pack;
 };
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
@@ -178,7 +181,27 @@ int resolve(const pkv_decode_desc* d, Resolved& r) {
     // more than 16 (the K/V tile is then read once for 32 rows).
     r.heads_per_wave = r.path == PKV_PATH_MFMA ? (r.rows > 16 ? 32 : 16) : valu_heads_per_wave(r.group);
     r.head_groups = static_cast<int>((r.rows + r.heads_per_wave - 1) / r.heads_per_wave);
+    r.kv_pack = 1;
     return PKV_OK;
+}
+
+// FP8 caches, one query token, no masks, head_dim up to 128, an even number of
+// KV heads whose query rows fit one MFMA block in pairs: a wave of the tile
+// schedule streams two adjacent KV heads (2 D contiguous bytes per token row
+// instead of D).  Measured on MI355X: see the FP8 section of the design notes.
+bool pairs_ok(const Resolved& r) {
+    return r.kv_fp8 && !r.multi_query && r.path == PKV_PATH_MFMA && r.M == 1 && r.Hk % 2 == 0 && 2 * r.rows <= 16 &&
+           r.D <= 128;
+}
+
+Resolved paired(Resolved r) {
+    r.kv_pack = 2;
+    r.Hk /= 2;
+    r.group *= 2;
+    r.rows *= 2;
+    r.heads_per_wave = 16;
+    r.head_groups = 1;
+    return r;
 }
 
 // How the work of one call is divided.
@@ -266,6 +289,23 @@ bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
                                : span_tiles;
     const int64_t share = items * (span_tiles + pkv::kHeaderTiles) / std::max(workers, 1);
     return single <= share + kCombineTiles;
+}
+
+SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits);
+
+// The plan of a call: resolve_splits, with KV heads paired (r updated) when
+// pairs_ok and the paired plan is the tile schedule; the single pass, split
+// schedules and the folded append stream one KV head per wave.
+SplitPlan plan_call(const pkv_decode_desc* d, Resolved& r, int num_splits, bool fold) {
+    if (!fold && pairs_ok(r)) {
+        const Resolved rp = paired(r);
+        const SplitPlan pp = resolve_splits(d, rp, num_splits);
+        if (pp.schedule == PKV_SCHED_TILES) {
+            r = rp;
+            return pp;
+        }
+    }
+    return resolve_splits(d, r, num_splits);
 }
 
 SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits) {
@@ -461,7 +501,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     if (num_splits < 0 || !std::isfinite(softmax_scale)) {
         return PKV_EINVAL;
     }
-    const SplitPlan plan = resolve_splits(desc, r, num_splits);
+    const SplitPlan plan = plan_call(desc, r, num_splits, fold != nullptr);
     const bool tiles = plan.schedule == PKV_SCHED_TILES;
     const int splits = tiles ? 0 : plan.splits;
     const size_t need = workspace_bytes(r, plan);
@@ -491,8 +531,8 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.part_lse = need > 0 ? reinterpret_cast<float*>(static_cast<char*>(desc->workspace) +
                                                      align_up(rows * static_cast<size_t>(r.D) * sizeof(float)))
                           : nullptr;
-    p.token_stride = r.Hk * r.D;
-    p.page_stride = r.P * r.Hk * r.D;
+    p.token_stride = r.Hk * r.kv_pack * r.D;
+    p.page_stride = r.P * r.Hk * r.kv_pack * r.D;
     p.num_heads = static_cast<int32_t>(r.H);
     p.num_heads_k = static_cast<int32_t>(r.Hk);
     p.group = static_cast<int32_t>(r.group);
@@ -525,6 +565,7 @@ int decode_impl(const void* q, const void* k_cache, const void* v_cache, const i
     p.alibi = desc->alibi_slopes;
     p.alibi_stride = desc->alibi_batch_stride;
     p.kv_fp8 = r.kv_fp8 ? 1 : 0;
+    p.kv_pack = r.kv_pack;
     p.k_scale = desc->k_scale;
     p.v_scale = desc->v_scale;
     p.lse = desc->softmax_lse;
@@ -701,7 +742,7 @@ int pkv_decode_num_splits(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    return resolve_splits(desc, r, num_splits).splits;
+    return plan_call(desc, r, num_splits, false).splits;
 }
 
 int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
@@ -709,7 +750,7 @@ int pkv_decode_split_tokens(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    return resolve_splits(desc, r, num_splits).split_tokens;
+    return plan_call(desc, r, num_splits, false).split_tokens;
 }
 
 int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits) {
@@ -717,7 +758,7 @@ int pkv_decode_schedule(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    return resolve_splits(desc, r, num_splits).schedule;
+    return plan_call(desc, r, num_splits, false).schedule;
 }
 
 int pkv_decode_path(const pkv_decode_desc* desc) {
@@ -733,7 +774,7 @@ size_t pkv_decode_workspace_size(const pkv_decode_desc* desc, int num_splits) {
     if (resolve(desc, r) != PKV_OK) {
         return 0;
     }
-    return workspace_bytes(r, resolve_splits(desc, r, num_splits));
+    return workspace_bytes(r, plan_call(desc, r, num_splits, false));
 }
 
 int pkv_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_table,
@@ -758,7 +799,7 @@ int pkv_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, 
     if (st != PKV_OK) {
         return st;
     }
-    if (num_splits >= 0 && workspace_bytes(r, resolve_splits(desc, r, num_splits)) > PKV_SCRATCH_BYTES) {
+    if (num_splits >= 0 && workspace_bytes(r, plan_call(desc, r, num_splits, false)) > PKV_SCRATCH_BYTES) {
         return PKV_ENOWORKSPACE;
     }
     void* ptr = nullptr;

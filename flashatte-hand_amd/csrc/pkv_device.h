@@ -57,6 +57,12 @@ struct PartitionParams {
     // Cache element type: 0 = the compute dtype (16-bit), 1 = OCP FP8 e4m3
     // (k / v then point at bytes) with per-KV-head fp32 scales (null = 1).
     int32_t kv_fp8;
+    // KV heads per stream: 1, or 2 (FP8 caches, tile schedule): a wave streams
+    // KV heads 2m and 2m + 1 together as one head of twice the width, so each
+    // token row it loads is 2 D contiguous bytes.  num_heads_k, group and rows
+    // then count these pairs (Hk / 2 of them, 2 group query heads each);
+    // token_stride and page_stride stay those of the cache.
+    int32_t kv_pack;
     const float* k_scale;
     const float* v_scale;
     float* lse;           // optional fp32 [B, H, M]: natural-log LSE of each output row (store_lse)

@@ -268,10 +268,22 @@ __device__ __forceinline__ int64_t query_out_row(const PartitionParams& p, int b
 // take the heads and columns 8-15 the remainders through one 16x16x16 MFMA,
 // and finish() adds column n + 8 to column n.  Otherwise both parts go along
 // K through a 16x16x32 MFMA whose A operand holds each V^T column twice.
-template <bool BF16, int D, bool MQ, int NB, bool COLS = false>
+//
+// KP = 2 (FP8 caches, one query token): the wave streams a pair of adjacent
+// KV heads as one head of D = 2 DH dims (DH the cache's head_dim).  Query
+// rows of the first head carry q in dims [0, DH) and zeros above, those of
+// the second the other way round, so one QK^T product over D gives every
+// row its own head's scores; O^T is computed over all D dims and each row
+// keeps its head's half.  Per-row K and V scales replace the wave-uniform
+// ones.
+template <bool BF16, int D, bool MQ, int NB, bool COLS = false, int KP = 1>
 struct MfmaMath {
     static_assert(!COLS || NB == 1, "column split: one block of at most 8 rows");
+    static_assert(KP == 1 || (KP == 2 && !MQ), "KV head pairs: one query token, no masks");
     static constexpr int kHeads = 16 * NB;
+    static constexpr int kPack = KP;
+    static constexpr int DH = D / KP;  // head_dim of the cache, q and out
+    static constexpr int DTH = DH / 16; // O^T tiles per head
     static constexpr int DT = D / 16;
     static constexpr bool kMultiQuery = MQ;
     static constexpr bool kBF16 = BF16;
@@ -303,6 +315,9 @@ struct MfmaMath {
         bool alibi;
         float cap;      // softcap in log2 units (0 = none) and its reciprocal
         float inv_cap;
+        int32_t sub[NB];    // KP = 2: which head of the pair the lane's row belongs to
+        float kscale[NB];   // KP = 2: K dequantisation scale of that head
+        float vscale[NB];   // KP = 2: V dequantisation scale of that head
     };
     // Per block: O^T tiles (lane (n, j): row n, dims 16 dt + 4j .. +3),
     // reference max, denominator.
@@ -327,6 +342,30 @@ struct MfmaMath {
     __device__ static void load_q(const PartitionParams& p, int b, int kvh, int r_first, int rows_here, int lane,
                                   Q& q) {
         const int j = lane >> 4;
+        if constexpr (KP == 2) {
+            // Rows 0 .. group / 2 - 1 belong to KV head 2 kvh, the rest to 2 kvh + 1.
+            const int per = p.group >> 1;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int n = 16 * nb + row_lane(lane);
+                const int s = min((r_first + n) / per, 1);
+                const int64_t row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
+                q.sub[nb] = s;
+                const int hk = 2 * kvh + s;
+                q.kscale[nb] = p.k_scale != nullptr ? p.k_scale[hk] : 1.f;
+                q.vscale[nb] = p.v_scale != nullptr ? p.v_scale[hk] : 1.f;
+#pragma unroll
+                for (int kk = 0; kk < D / 32; ++kk) {
+                    const int half = kk / (DH / 32);
+                    if (n < rows_here && half == s) {
+                        q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * DH + 8 * (4 * (kk - half * (DH / 32)) + j));
+                    } else {
+                        q.op[nb][kk] = make_uint4(0u, 0u, 0u, 0u);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int n = 16 * nb + row_lane(lane);
@@ -465,9 +504,10 @@ struct MfmaMath {
         if (plain) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
+                const float sl = KP == 2 ? scale_log2 * q.kscale[nb] : scale_log2;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    sc[nb][i] = (t0 + 4 * j + i) < end ? s[nb][i] * scale_log2 : kNegInf;
+                    sc[nb][i] = (t0 + 4 * j + i) < end ? s[nb][i] * sl : kNegInf;
                 }
             }
         } else {
@@ -603,20 +643,23 @@ struct MfmaMath {
         for (int nb = 0; nb < NB; ++nb) {
             const int n = 16 * nb + (lane & 15);
             if (n < heads_here) {
-                const float inv = a.l[nb] > 0.f ? out_scale / a.l[nb] : 0.f;
+                const float inv = a.l[nb] > 0.f ? (KP == 2 ? q.vscale[nb] : out_scale) / a.l[nb] : 0.f;
                 int64_t row;
                 if constexpr (MQ) {
                     row = q.row[nb];
                 } else {
                     row = bh_first + n;
                 }
-                uint16_t* dst = p.out + row * D + 4 * j;
+                uint16_t* dst = p.out + row * DH + 4 * j;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
+                    if (KP == 2 && dt / DTH != q.sub[nb]) {
+                        continue; // the other head's half of the pair
+                    }
                     uint2 w;
                     w.x = pack2<BF16>(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv);
                     w.y = pack2<BF16>(a.o[nb][dt][2] * inv, a.o[nb][dt][3] * inv);
-                    *reinterpret_cast<uint2*>(dst + 16 * dt) = w;
+                    *reinterpret_cast<uint2*>(dst + 16 * (dt % DTH)) = w;
                 }
                 if (p.lse != nullptr && j == 0) {
                     store_lse(p.lse, row, p.q_len, p.num_heads, a.m[nb] - kProbLog2Offset, a.l[nb]);
@@ -627,7 +670,7 @@ struct MfmaMath {
 
     // Partial of slice row h at index part_base + h * part_stride: O / l in
     // fp32 and the log2-domain LSE m + log2(l).
-    __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
+    __device__ static void write_partial(const PartitionParams& p, const Q& q, int64_t part_base, int64_t part_stride,
                                          int heads_here, const Acc& a, int lane, float out_scale) {
         const int j = lane >> 4;
 #pragma unroll
@@ -635,11 +678,14 @@ struct MfmaMath {
             const int n = 16 * nb + (lane & 15);
             if (n < heads_here) {
                 const int64_t pi = part_base + n * part_stride;
-                const float inv = a.l[nb] > 0.f ? out_scale / a.l[nb] : 0.f;
-                float* dst = p.part_o + pi * D + 4 * j;
+                const float inv = a.l[nb] > 0.f ? (KP == 2 ? q.vscale[nb] : out_scale) / a.l[nb] : 0.f;
+                float* dst = p.part_o + pi * DH + 4 * j;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    *reinterpret_cast<float4*>(dst + 16 * dt) =
+                    if (KP == 2 && dt / DTH != q.sub[nb]) {
+                        continue;
+                    }
+                    *reinterpret_cast<float4*>(dst + 16 * (dt % DTH)) =
                         make_float4(a.o[nb][dt][0] * inv, a.o[nb][dt][1] * inv, a.o[nb][dt][2] * inv,
                                     a.o[nb][dt][3] * inv);
                 }
@@ -714,6 +760,7 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
 template <bool BF16, int D, int NH>
 struct ValuMath {
     static constexpr int kHeads = NH;
+    static constexpr int kPack = 1;
     static constexpr int E = D / 64; // output dims per lane and head
     static constexpr bool kMultiQuery = false; // one query token, no mask
     static constexpr bool kBF16 = BF16;
@@ -859,7 +906,7 @@ struct ValuMath {
         }
     }
 
-    __device__ static void write_partial(const PartitionParams& p, int64_t part_base, int64_t part_stride,
+    __device__ static void write_partial(const PartitionParams& p, const Q&, int64_t part_base, int64_t part_stride,
                                          int heads_here, const Acc& a, int lane, float out_scale) {
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
@@ -1032,10 +1079,10 @@ struct KvScales {
     float out;        // v_scale
 };
 
-template <bool FP8>
+template <bool FP8, int KP = 1>
 __device__ __forceinline__ KvScales kv_scales(const PartitionParams& p, int kvh) {
     KvScales s{p.scale_log2, 1.f};
-    if constexpr (FP8) {
+    if constexpr (FP8 && KP == 1) { // pairs of KV heads: per-row scales in the Math's Q
         if (p.k_scale != nullptr) {
             s.score_log2 *= p.k_scale[kvh];
         }
@@ -1126,7 +1173,7 @@ void partition_split_kernel(PartitionParams p) {
     if (p.splits == 1) {
         Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
     } else {
-        Math::write_partial(p, sr_first * p.splits + split, p.splits, heads_here, acc, lane, ks.out);
+        Math::write_partial(p, q, sr_first * p.splits + split, p.splits, heads_here, acc, lane, ks.out);
     }
 }
 
@@ -1205,7 +1252,7 @@ void partition_item_group_kernel(PartitionParams p) {
     if (p.splits == 1) {
         Math::write_final(p, q, bh_first, heads_here, acc, lane, ks.out);
     } else {
-        Math::write_partial(p, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane, ks.out);
+        Math::write_partial(p, q, sr_first * p.splits + it.split, p.splits, heads_here, acc, lane, ks.out);
     }
 }
 
@@ -1268,7 +1315,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 if (pend_final) {
                     Math::write_final(p, pend_q, pend_at, pend_heads, pend_acc, lane, pend_scale);
                 } else {
-                    Math::write_partial(p, pend_at, 1, pend_heads, pend_acc, lane, pend_scale);
+                    Math::write_partial(p, pend_q, pend_at, 1, pend_heads, pend_acc, lane, pend_scale);
                 }
                 pending = false;
             }
@@ -1294,7 +1341,7 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 const int win_base = begin >> p.page_shift;
                 const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
-                const KvScales ks = kv_scales<FP8>(p, kvh);
+                const KvScales ks = kv_scales<FP8, Math::kPack>(p, kvh);
                 typename Math::Acc acc;
                 attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc,
                                                         ks.score_log2, flush);
@@ -1389,6 +1436,21 @@ static void launch_math_kv(const PartitionParams& p, hipStream_t stream, const L
     }
 }
 
+// Pairs of KV heads (FP8 caches, tile schedule): the paired Math over the
+// pair's 2 DH dims.
+template <typename Math, int D>
+static hipError_t launch_pairs(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
+    if (p.tile_workers <= 0 || !p.kv_fp8) {
+        return hipErrorInvalidValue;
+    }
+    if (p.page_shift >= 4) {
+        launch_tiles<Math, D, true, true>(p, stream, ev);
+    } else {
+        launch_tiles<Math, D, false, true>(p, stream, ev);
+    }
+    return hipGetLastError();
+}
+
 // FP8 caches only with the MFMA policies.
 template <typename Math, int D>
 static hipError_t launch_math(const PartitionParams& p, hipStream_t stream, const LaunchEvents& ev) {
@@ -1410,6 +1472,18 @@ static hipError_t launch_d(const PartitionParams& p, bool mfma, int heads_per_wa
     const bool multi_query =
         p.q_len > 1 || p.win_left >= 0 || p.win_right >= 0 || p.alibi != nullptr || p.softcap_log2 > 0.f ||
         p.kv_start != nullptr;
+    if (mfma && p.kv_pack == 2) {
+        // A pair of KV heads per wave: rows = 2 group <= 16 query rows.
+        if constexpr (D <= 128) {
+            if (multi_query || p.rows > 16) {
+                return hipErrorInvalidValue;
+            }
+            return p.rows <= 8 ? launch_pairs<MfmaMath<BF16, 2 * D, false, 1, true, 2>, 2 * D>(p, stream, ev)
+                               : launch_pairs<MfmaMath<BF16, 2 * D, false, 1, false, 2>, 2 * D>(p, stream, ev);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     if (mfma) {
         // 16 or 32 query rows per wave (heads_per_wave).
         if (heads_per_wave == 32) {

@@ -95,9 +95,12 @@ def test_fp8_cache_matches_oracle(rng, splits, B, H, Hk, D, P, seqlens, dtype, M
     assert_close(out, want, dtype)
 
 
-@pytest.mark.parametrize("splits", [0, 1, 4])
+@pytest.mark.parametrize("splits", [1, 4])
 @pytest.mark.parametrize("dtype", [0, 1])
 def test_fp8_with_unit_scales_reproduces_the_16bit_bits(rng, splits, dtype):
+    """The single pass and page splits read FP8 rows exactly as the 16-bit path reads their
+    values.  (The heuristic's tile schedule streams FP8 KV heads in pairs, which cuts the
+    streams differently from the 16-bit path; it is checked against the oracle instead.)"""
     import pagedkv
 
     torch = torch_mod()
@@ -185,3 +188,49 @@ def test_decode_append_on_fp8_cache(rng):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(from_dev8(dk), want_k)
     assert_close(out, want, dtype)
+
+
+PAIRS = [
+    # B, H, Hk, D, P, row lengths, dtype, scales: tile-schedule shapes whose KV heads the FP8 path
+    # streams in pairs (group 4: 8 rows per pair, the column-split MFMA form; group 8: 16 rows;
+    # head_dim 64 and 128; pages of 64, 16 and 8 tokens; one-token and empty rows)
+    (24, 32, 8, 128, 64, None, 1, True),
+    (16, 64, 8, 128, 16, None, 0, True),
+    (24, 16, 4, 64, 8, None, 1, False),
+    (20, 32, 8, 128, 16, [1, 0, 17, 4000], 1, True),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PAIRS)))
+def test_fp8_kv_head_pairs_on_the_tile_schedule(case):
+    """FP8 caches on the tile schedule: each wave streams two adjacent KV heads (one token row
+    of 2 head_dim bytes per load), each query row scoring and averaging its own head's half with
+    its own head's K / V scales.  Outputs and softmax_lse against the fp64 oracle; the plan is
+    checked to be the tile schedule with its combine."""
+    import pagedkv
+    from test_gpu_lse import assert_lse, lse_buffer
+
+    torch = torch_mod()
+    B, H, Hk, D, P, lens, dtype, scaled = PAIRS[case]
+    announce("fp8-pairs", PAIRS[case])
+    rng = np.random.default_rng(9100 + case)
+    sl = rng.integers(300, 3000, B).astype(np.int32)
+    if lens is not None:
+        sl[:len(lens)] = lens
+    _, k16, _, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=sl, dtype=dtype)
+    ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32) if scaled else None
+    vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32) if scaled else None
+    k8 = fp8_cache(rng, k16.shape, ks)
+    v8 = fp8_cache(rng, k16.shape, vs)
+    q = rand_bits(rng, (B, 1, H, D), dtype)
+    scale = 1.0 / math.sqrt(D)
+    desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=k8.shape[0],
+                             block_table_stride=bt.shape[1], dtype=dtype, kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3)
+    assert pagedkv.schedule_for(desc, 0) == pagedkv.PKV_SCHED_TILES
+    lse = lse_buffer(B, H, 1)
+    out = pagedkv.decode(to_dev(q, dtype), to_dev8(k8), to_dev8(v8), i32(bt), i32(sl), scale, 0, k_scale=f32(ks),
+                         v_scale=f32(vs), softmax_lse=lse)
+    torch.cuda.synchronize()
+    want, want_lse = po.attn8_f64(q, k8, v8, bt, sl, scale, dtype, k_scale=ks, v_scale=vs, lse=True)
+    assert_close(out, want, dtype)
+    assert_lse(lse, want_lse)
