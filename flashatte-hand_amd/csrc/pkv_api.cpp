@@ -293,14 +293,26 @@ bool single_pass_wins(const Resolved& r, int64_t max_seqlen, int workers) {
 
 SplitPlan resolve_splits(const pkv_decode_desc* d, const Resolved& r, int num_splits);
 
+// Paired KV heads make a wave's share half as many (twice as wide) units, so
+// each segment's start-up (page window, first tile) weighs twice as much.
+// They pay off when a wave's share, bounded from max_seqlen, holds at least
+// this many paired units.  Measured on MI355X with FP8 caches, paired /
+// one head per wave (µs per call, the timed loop's repeats): C3 (128 units)
+// 109.0 / 117.1, C4 (513) 127.4 / 130.0, C2 (32) 33.2 / 32.1.
+constexpr int64_t kPairMinShare = 64;
+
 // The plan of a call: resolve_splits, with KV heads paired (r updated) when
-// pairs_ok and the paired plan is the tile schedule; the single pass, split
-// schedules and the folded append stream one KV head per wave.
+// pairs_ok and the paired plan is the tile schedule with long shares; the
+// single pass, split schedules and the folded append stream one KV head per
+// wave.
 SplitPlan plan_call(const pkv_decode_desc* d, Resolved& r, int num_splits, bool fold) {
     if (!fold && pairs_ok(r)) {
         const Resolved rp = paired(r);
         const SplitPlan pp = resolve_splits(d, rp, num_splits);
-        if (pp.schedule == PKV_SCHED_TILES) {
+        const int64_t share = rp.B * streams_per_row(rp) *
+                              (row_tiles_bound(rp, effective_max_seqlen(d, rp)) + pkv::kHeaderTiles) /
+                              std::max(pp.splits, 1);
+        if (pp.schedule == PKV_SCHED_TILES && share >= kPairMinShare) {
             r = rp;
             return pp;
         }

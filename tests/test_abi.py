@@ -186,6 +186,39 @@ def test_tile_schedule_plan():
     assert pagedkv.workspace_size(v, 0) == align(rows * 128 * 4) + align(rows * 4)
 
 
+def test_fp8_kv_head_pairs_in_the_plan():
+    """FP8 caches on the tile schedule stream two adjacent KV heads per wave when a wave's share
+    (bounded from max_seqlen) holds at least 64 paired units: the partial slots then hold the
+    pair's 2 x group rows for half as many streams.  Short shares, 16-bit caches, an odd KV head
+    count, masks and several query tokens keep one KV head per wave."""
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+
+    def slots(desc, hk_streams, group_rows):
+        workers = pagedkv.num_splits_for(desc, 0)
+        rows = (workers + desc.batch * hk_streams) * group_rows
+        return align(rows * desc.head_dim * 4) + align(rows * 4)
+
+    fp8 = pagedkv.PKV_KV_DTYPE_FP8_E4M3
+    # long shares (C3-like: 4 rows of up to 131072 tokens): pairs, 8 rows per partial slot
+    long_ = base_desc(batch=4, max_seqlen=131072, block_table_stride=2048, kv_dtype=fp8)
+    assert pagedkv.schedule_for(long_, 0) == pagedkv.PKV_SCHED_TILES
+    assert pagedkv.workspace_size(long_, 0) == slots(long_, 4, 8)
+    # the same shape with 16-bit caches: one head per wave
+    assert pagedkv.workspace_size(base_desc(batch=4, max_seqlen=131072, block_table_stride=2048), 0) == \
+        slots(base_desc(batch=4, max_seqlen=131072, block_table_stride=2048), 8, 4)
+    # short shares (C2-like: 32 rows of up to 4096 tokens, 32 paired units per wave): one head per wave
+    short = base_desc(max_seqlen=4096, kv_dtype=fp8)
+    assert pagedkv.workspace_size(short, 0) == slots(short, 8, 4)
+    # group 8 (C4-like): 16-row pairs
+    g8 = base_desc(batch=128, num_heads=64, max_seqlen=16384, block_table_stride=512, page_size=32, kv_dtype=fp8)
+    assert pagedkv.workspace_size(g8, 0) == slots(g8, 4, 16)
+    # an odd KV head count, two query tokens, a causal mask: no pairs
+    odd = base_desc(batch=4, num_heads=12, num_heads_k=3, max_seqlen=131072, block_table_stride=2048, kv_dtype=fp8)
+    assert pagedkv.workspace_size(odd, 0) == slots(odd, 3, 4)
+    two = base_desc(batch=4, max_seqlen=131072, block_table_stride=2048, kv_dtype=fp8, seqlen_q=2)
+    assert pagedkv.workspace_size(two, 0) == slots(two, 8, 8)
+
+
 # The evaluator's contest shapes (B, longest row, KV heads; 32 query heads, head_dim 128, page size
 # 16, bf16; scripts/evaluate_flashattn_submission.py:359-389) and the schedule the num_splits = 0
 # heuristic takes for each, as the reference's run_kernel passes them (max_seqlen = seqlen_k, a

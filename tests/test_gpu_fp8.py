@@ -205,8 +205,10 @@ PAIRS = [
 def test_fp8_kv_head_pairs_on_the_tile_schedule(case):
     """FP8 caches on the tile schedule: each wave streams two adjacent KV heads (one token row
     of 2 head_dim bytes per load), each query row scoring and averaging its own head's half with
-    its own head's K / V scales.  Outputs and softmax_lse against the fp64 oracle; the plan is
-    checked to be the tile schedule with its combine."""
+    its own head's K / V scales.  A max_seqlen hint of 65536 makes the shares long enough for the
+    pairs (tests/test_abi.py checks the rule); the rows themselves are short.  Outputs and
+    softmax_lse against the fp64 oracle; the plan is checked to be the paired tile schedule (its
+    partial slots hold 2 x group rows)."""
     import pagedkv
     from test_gpu_lse import assert_lse, lse_buffer
 
@@ -217,7 +219,8 @@ def test_fp8_kv_head_pairs_on_the_tile_schedule(case):
     sl = rng.integers(300, 3000, B).astype(np.int32)
     if lens is not None:
         sl[:len(lens)] = lens
-    _, k16, _, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=sl, dtype=dtype)
+    hint = 1 << 16  # block-table rows as wide as the hint, so it bounds the rows
+    _, k16, _, bt, sl = make_case(rng, B=B, H=H, Hk=Hk, D=D, P=P, seqlens=sl, dtype=dtype, stride=hint // P)
     ks = rng.uniform(0.2, 2.0, Hk).astype(np.float32) if scaled else None
     vs = rng.uniform(0.2, 2.0, Hk).astype(np.float32) if scaled else None
     k8 = fp8_cache(rng, k16.shape, ks)
@@ -225,11 +228,14 @@ def test_fp8_kv_head_pairs_on_the_tile_schedule(case):
     q = rand_bits(rng, (B, 1, H, D), dtype)
     scale = 1.0 / math.sqrt(D)
     desc = pagedkv.make_desc(batch=B, num_heads=H, num_heads_k=Hk, head_dim=D, page_size=P, num_pages=k8.shape[0],
-                             block_table_stride=bt.shape[1], dtype=dtype, kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3)
+                             block_table_stride=bt.shape[1], dtype=dtype, kv_dtype=pagedkv.PKV_KV_DTYPE_FP8_E4M3,
+                             max_seqlen=hint)
     assert pagedkv.schedule_for(desc, 0) == pagedkv.PKV_SCHED_TILES
+    rows = (pagedkv.num_splits_for(desc, 0) + B * Hk // 2) * 2 * (H // Hk)
+    assert pagedkv.workspace_size(desc, 0) == -(-rows * D * 4 // 256) * 256 + -(-rows * 4 // 256) * 256
     lse = lse_buffer(B, H, 1)
     out = pagedkv.decode(to_dev(q, dtype), to_dev8(k8), to_dev8(v8), i32(bt), i32(sl), scale, 0, k_scale=f32(ks),
-                         v_scale=f32(vs), softmax_lse=lse)
+                         v_scale=f32(vs), softmax_lse=lse, max_seqlen=hint)
     torch.cuda.synchronize()
     want, want_lse = po.attn8_f64(q, k8, v8, bt, sl, scale, dtype, k_scale=ks, v_scale=vs, lse=True)
     assert_close(out, want, dtype)
