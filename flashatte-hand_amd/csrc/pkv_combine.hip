@@ -164,7 +164,24 @@ __device__ __forceinline__ RowUnits row_units(const CombineParams& p, int32_t b,
     int64_t before = 0;
     int64_t all = 0;
     int32_t nb = 0;
-    for (int32_t bb = lane; bb < p.batch; bb += 64) {
+    // The first kScanChunks * 64 rows: every load out before any is used, with no
+    // branch around them (lanes past the batch re-read its last row and are
+    // dropped), so they cost one round trip, not one per chunk.
+    int32_t raw[kScanChunks];
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        raw[c] = p.seqlens[min(64 * c + lane, p.batch - 1)];
+    }
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        const int32_t bb = 64 * c + lane;
+        const int32_t n = bb < p.batch ? tile_span(min(max(raw[c], 0), p.row_cap), p.q_len, p.win_left).n : 0;
+        const int32_t t = stream_units(n);
+        all += t;
+        before += bb < b ? t : 0;
+        nb = bb == b ? n : nb;
+    }
+    for (int32_t bb = lane + 64 * kScanChunks; bb < p.batch; bb += 64) {
         const int32_t n = row_tiles(p.seqlens, bb, p.row_cap, p.q_len, p.win_left);
         const int32_t t = stream_units(n);
         all += t;

@@ -647,10 +647,18 @@ __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens
     // Units of one stream are below 2^27 (row_cap < 2^31 tokens), so a chunk
     // of 64 rows of them fits 32 bits when row_cap <= 2^24.
     rs.fast = batch <= 64 * kScanChunks && row_cap <= (1 << 24);
+    // Every chunk's load goes out before any is used, with no branch around it
+    // (lanes past the batch re-read its last row; a select drops them): a load
+    // under a branch would make the compiler wait for each chunk in turn.
+    int32_t raw[kScanChunks];
+#pragma unroll
+    for (int c = 0; c < kScanChunks; ++c) {
+        raw[c] = seqlens[min(64 * c + lane, batch - 1)];
+    }
 #pragma unroll
     for (int c = 0; c < kScanChunks; ++c) {
         const int32_t b = 64 * c + lane;
-        rs.sl[c] = (c == 0 || 64 * c < batch) && b < batch ? clamped_seqlen(seqlens, b, row_cap) : 0;
+        rs.sl[c] = b < batch ? min(max(raw[c], 0), row_cap) : 0;
         rs.n[c] = tile_span(rs.sl[c], q_len, win_left).n;
     }
     if (rs.fast) {
@@ -682,6 +690,23 @@ __device__ __forceinline__ RowScan scan_rows(const int32_t* __restrict__ seqlens
     }
     rs.rows_total = wave_sum_i64(sum);
     return rs;
+}
+
+// Clamped seqlen of row b (wave-uniform b): from the scan's registers when
+// they hold every row, else from cache_seqlens (one dependent load).
+__device__ __forceinline__ int32_t scanned_seqlen(const RowScan& rs, const int32_t* __restrict__ seqlens, int32_t b,
+                                                  int32_t row_cap) {
+    if (rs.fast) {
+        int32_t v = 0;
+#pragma unroll
+        for (int c = 0; c < kScanChunks; ++c) {
+            if ((b >> 6) == c) {
+                v = __builtin_amdgcn_readlane(rs.sl[c], b & 63);
+            }
+        }
+        return v;
+    }
+    return __builtin_amdgcn_readfirstlane(clamped_seqlen(seqlens, b, row_cap));
 }
 
 // Row holding stream-unit index y (0 <= y < rows_total).
@@ -747,11 +772,15 @@ __device__ __forceinline__ int64_t uniform(int64_t x) {
 // a dependent global load would force the wave to drain (vmcnt is in order)
 // every K/V load it has in flight.  Out-of-range ids are clamped to page 0 so a
 // corrupt table cannot fault the GPU; entries past the row's last page are 0
-// and never used.
+// and never used.  Every lane loads (lanes past the last page re-read it) and a
+// select drops the extra entries: a load under a branch would make the
+// compiler's later waits count every load issued since as outstanding work to
+// drain, so the first tile's addresses would also wait for q.
 __device__ __forceinline__ int32_t load_page_window(const int32_t* __restrict__ bt_row, int32_t base,
                                                     int32_t last_page, int32_t lane, int32_t num_pages) {
     const int32_t idx = base + lane;
-    const int32_t v = idx <= last_page ? bt_row[idx] : 0;
+    const int32_t e = bt_row[min(idx, last_page)];
+    const int32_t v = idx <= last_page ? e : 0;
     return static_cast<uint32_t>(v) < static_cast<uint32_t>(num_pages) ? v : 0;
 }
 

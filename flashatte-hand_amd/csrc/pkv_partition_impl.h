@@ -349,19 +349,21 @@ struct MfmaMath {
             for (int nb = 0; nb < NB; ++nb) {
                 const int n = 16 * nb + row_lane(lane);
                 const int s = min((r_first + n) / per, 1);
-                const int64_t row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
                 q.sub[nb] = s;
                 const int hk = 2 * kvh + s;
                 q.kscale[nb] = p.k_scale != nullptr ? p.k_scale[hk] : 1.f;
                 q.vscale[nb] = p.v_scale != nullptr ? p.v_scale[hk] : 1.f;
+                // Loads on every lane (rows past the slice read its last row), then a
+                // select: no branch, so the compiler's wait for the page window,
+                // issued before them, does not also wait for q.
+                const int64_t lrow =
+                    static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + min(n, rows_here - 1);
 #pragma unroll
                 for (int kk = 0; kk < D / 32; ++kk) {
                     const int half = kk / (DH / 32);
-                    if (n < rows_here && half == s) {
-                        q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * DH + 8 * (4 * (kk - half * (DH / 32)) + j));
-                    } else {
-                        q.op[nb][kk] = make_uint4(0u, 0u, 0u, 0u);
-                    }
+                    const uint4 v = *reinterpret_cast<const uint4*>(p.q + lrow * DH + 8 * (4 * (kk % (DH / 32)) + j));
+                    const bool keep = n < rows_here && half == s;
+                    q.op[nb][kk] = keep ? v : make_uint4(0u, 0u, 0u, 0u);
                 }
             }
             return;
@@ -377,15 +379,15 @@ struct MfmaMath {
                 row = (static_cast<int64_t>(b) * p.q_len + q.qi[nb]) * p.num_heads + q.head[nb];
                 q.row[nb] = row;
             } else {
-                row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + n;
+                row = static_cast<int64_t>(b) * p.num_heads + kvh * p.group + r_first + min(n, rows_here - 1);
             }
+            // Rows past the slice repeat its last row: their MFMA columns are never
+            // written, and with no branch and no select on the loaded values the
+            // compiler's wait for the page window (issued before) does not also
+            // wait for q, which is first needed after the first tile lands.
 #pragma unroll
             for (int kk = 0; kk < D / 32; ++kk) {
-                if (n < rows_here) {
-                    q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
-                } else {
-                    q.op[nb][kk] = make_uint4(0u, 0u, 0u, 0u);
-                }
+                q.op[nb][kk] = *reinterpret_cast<const uint4*>(p.q + row * D + 8 * (4 * kk + j));
             }
         }
     }
@@ -786,11 +788,10 @@ struct ValuMath {
         const int64_t bh_first = out_row(p, b, kvh, r_first);
 #pragma unroll
         for (int h = 0; h < NH; ++h) {
+            const int hl = min(h, heads_here - 1); // heads past the slice repeat its last (never written)
 #pragma unroll
             for (int i = 0; i < D / 32; ++i) {
-                q.q[h][i] = h < heads_here
-                                ? *reinterpret_cast<const uint4*>(p.q + (bh_first + h) * D + 8 * (4 * i + c))
-                                : make_uint4(0u, 0u, 0u, 0u);
+                q.q[h][i] = *reinterpret_cast<const uint4*>(p.q + (bh_first + hl) * D + 8 * (4 * i + c));
             }
         }
     }
@@ -1335,11 +1336,14 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 const int begin = (first + t_lo) * 16;
                 const int end = min((first + t_hi) * 16, seqlen);
 
+                // The page window's load goes out before q's: the first tile's
+                // addresses wait for the window only (vmcnt counts in order), and q
+                // is first needed after that tile has landed.
+                const int win_base = begin >> p.page_shift;
+                const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
                 typename Math::Q q;
                 Math::load_q(p, b, kvh, r_first, heads_here, lane, q);
                 Math::set_mask(p, b, seqlen, heads_here, lane, q);
-                const int win_base = begin >> p.page_shift;
-                const int win = load_page_window(bt_row, win_base, (end - 1) >> p.page_shift, lane, p.num_pages);
 
                 const KvScales ks = kv_scales<FP8, Math::kPack>(p, kvh);
                 typename Math::Acc acc;
@@ -1360,12 +1364,13 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                 flush();
                 break;
             }
-            // Next super-stream, past rows without tokens (they own no units).
+            // Next super-stream, past rows without tokens (they own no units); the
+            // row lengths come from the scan's registers (no load) up to 256 rows.
             if (++u == sps) {
                 u = 0;
                 do {
                     ++b;
-                    seqlen = uniform(clamped_seqlen(p.seqlens, b, p.row_cap));
+                    seqlen = scanned_seqlen(scan, p.seqlens, b, p.row_cap);
                 } while (seqlen == 0 && b + 1 < p.batch);
                 const TileSpan span = tile_span(seqlen, p.q_len, p.win_left);
                 first = span.first;
