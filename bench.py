@@ -131,8 +131,8 @@ def run_config(name: str, args, torch, pagedkv, events: HipEvents) -> dict:
     if fp8:
         # OCP FP8 e4m3 caches with per-KV-head scales: the same shapes at one byte per element.
         for s_ in sets:
-            for name in ("k_cache", "v_cache"):
-                s_[name] = s_[name].float().clamp(-448, 448).to(torch.float8_e4m3fn)
+            for cache in ("k_cache", "v_cache"):
+                s_[cache] = s_[cache].float().clamp(-448, 448).to(torch.float8_e4m3fn)
             s_["k_scale"] = torch.rand(cfg.num_heads_k, device="cuda") + 0.5
             s_["v_scale"] = torch.rand(cfg.num_heads_k, device="cuda") + 0.5
     if M > 1:
