@@ -1303,7 +1303,12 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
         int64_t vs = row_first + static_cast<int64_t>(u) * units; // first unit of super-stream (b, u)
         // A finished segment's rows (output or partial) are stored once the
         // next segment's first tile loads are out, so their stores do not hold
-        // up that segment's first waits; the last segment's at the end.
+        // up that segment's first waits; the last segment's at the end.  The
+        // held copy of q and the accumulator costs their registers a second
+        // time: a math of two 16-row blocks at head_dim 256 (132 accumulator
+        // floats per lane) would spill, so it stores each segment's rows at
+        // once.
+        constexpr bool kDefer = Math::kAccFloats <= 72;
         typename Math::Q pend_q;
         typename Math::Acc pend_acc;
         int64_t pend_at = 0; // output row of the slice (final) or partial index of row 0
@@ -1347,17 +1352,29 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
 
                 const KvScales ks = kv_scales<FP8, Math::kPack>(p, kvh);
                 typename Math::Acc acc;
-                attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh, acc,
-                                                        ks.score_log2, flush);
-                pend_final = t_lo == 0 && t_hi == nb && !p.force_partial;
-                pend_at = pend_final ? bh_first
-                                     : (((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j) *
-                                           p.part_heads;
-                pend_q = q;
-                pend_acc = acc;
-                pend_heads = heads_here;
-                pend_scale = ks.out;
-                pending = true;
+                const bool whole = t_lo == 0 && t_hi == nb && !p.force_partial;
+                const int64_t at = whole ? bh_first
+                                         : (((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j) *
+                                               p.part_heads;
+                if constexpr (kDefer) {
+                    attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh,
+                                                            acc, ks.score_log2, flush);
+                    pend_final = whole;
+                    pend_at = at;
+                    pend_q = q;
+                    pend_acc = acc;
+                    pend_heads = heads_here;
+                    pend_scale = ks.out;
+                    pending = true;
+                } else {
+                    attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh,
+                                                            acc, ks.score_log2);
+                    if (whole) {
+                        Math::write_final(p, q, at, heads_here, acc, lane, ks.out);
+                    } else {
+                        Math::write_partial(p, q, at, 1, heads_here, acc, lane, ks.out);
+                    }
+                }
             }
             vs += units;
             if (vs >= x_end) {
