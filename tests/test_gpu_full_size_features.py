@@ -1,4 +1,4 @@
-"""The BASELINE configs at full size with FP8 caches, the C2 / C4 shapes as a speculative
+"""The BASELINE configs at full size with FP8 caches, the C2 / C4 / C5 shapes as a speculative
 verify step (four causal query tokens), and C2 / C5 with a sliding window and ALiBi, on the
 heuristic schedule: every output row and its softmax_lse against the fp64 oracle (OpenMP over
 rows on the host), as tests/test_gpu_parity.py checks the 16-bit one-token decode.
@@ -49,7 +49,9 @@ def test_full_size_config_with_fp8_caches(name):
     assert_lse(lse, want_lse)
 
 
-@pytest.mark.parametrize("name", ["c2", "c4"])
+# C5: 16 query heads per KV head at head_dim 256, so four tokens make 64 rows per KV head: two
+# head groups of two 16-row blocks each, the math that stores every segment at once.
+@pytest.mark.parametrize("name", ["c2", "c4", "c5"])
 def test_full_size_config_as_causal_verify_step(name):
     import pagedkv
     from pagedkv.configs import make_config, make_tensors
