@@ -95,16 +95,25 @@ struct TileRegs {
     Chunk v[NI];
 };
 
-// One lane's chunk of a token row: 16 bytes of 16-bit values, or 8 FP8 bytes;
-// nontemporal (the cache is streamed once).
-template <bool FP8>
+// One lane's chunk of a token row: 16 bytes of 16-bit values, or 8 FP8 bytes.
+// NT: nontemporal, for a cache streamed once.  Without it the lines stay in
+// the L2 for the other waves of a gang that read the same tokens (several head
+// groups of one KV head).  Measured on MI355X with four or eight causal query
+// tokens (64-128 rows per KV head, two to four head groups per gang), plain /
+// nontemporal: C5 251.8 / 284.7 and 387.5 / 439.7 µs, C4 366.1 / 383.8 µs; one
+// head group per wave (C2, eight tokens) 72.6 / 64.4 µs.
+template <bool FP8, bool NT = true>
 __device__ __forceinline__ typename TileRegs<64, FP8>::Chunk load_chunk(const char* ptr) {
     if constexpr (FP8) {
         typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-        const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(ptr));
+        const u32x2_t v = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(ptr))
+                             : *reinterpret_cast<const u32x2_t*>(ptr);
         return make_uint2(v.x, v.y);
-    } else {
+    } else if constexpr (NT) {
         return load_kv16(reinterpret_cast<const uint16_t*>(ptr));
+    } else {
+        const uint4 v = *reinterpret_cast<const uint4*>(ptr);
+        return v;
     }
 }
 
@@ -126,7 +135,7 @@ __device__ __forceinline__ typename TileRegs<64, FP8>::Chunk load_chunk(const ch
 // through a per-tile descriptor — one 32-bit offset per lane, rows past the
 // range read as zeros — cut the loop's VALU from 86 to 67 per tile but
 // measured 1-4 % slower.)
-template <int D, bool WIDE, bool FP8>
+template <int D, bool WIDE, bool FP8, bool NT = true>
 __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionParams& p, int win, int win_base,
                                           int t0, int end, bool real, int lane, int kvh) {
     using Regs = TileRegs<D, FP8>;
@@ -157,8 +166,8 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const uint32_t off = min(static_cast<uint32_t>(R * i + rl) * ts2 + col, lim_off);
-            r.k[i] = load_chunk<FP8>(kb + off);
-            r.v[i] = load_chunk<FP8>(vb + off);
+            r.k[i] = load_chunk<FP8, NT>(kb + off);
+            r.v[i] = load_chunk<FP8, NT>(vb + off);
         }
     } else {
 #pragma unroll
@@ -168,8 +177,8 @@ __device__ __forceinline__ void load_tile(TileRegs<D, FP8>& r, const PartitionPa
             const int64_t off =
                 real ? static_cast<int64_t>(phys) * p.page_stride * EB + static_cast<int64_t>(t & pmask) * ts2 + col
                      : 0;
-            r.k[i] = load_chunk<FP8>(reinterpret_cast<const char*>(p.k) + off);
-            r.v[i] = load_chunk<FP8>(reinterpret_cast<const char*>(p.v) + off);
+            r.k[i] = load_chunk<FP8, NT>(reinterpret_cast<const char*>(p.k) + off);
+            r.v[i] = load_chunk<FP8, NT>(reinterpret_cast<const char*>(p.v) + off);
         }
     }
 }
@@ -983,7 +992,8 @@ struct NoWork {
 // hold up the first wait, such as the previous segment's output stores
 // (vmcnt counts stores too, so a store issued before a load delays the wait
 // for that load until the store completes).
-template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD, bool FP8, typename After = NoWork>
+template <typename Math, int D, bool WIDE, int DEPTH, bool RELOAD, bool FP8, bool NT = true,
+          typename After = NoWork>
 __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_t* __restrict__ bt_row, int last_page,
                                           int& win, int& win_base, const typename Math::Q& q,
                                           typename Math::Acc& acc, uint16_t* lds, int t, int end, int lane,
@@ -1007,11 +1017,11 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
     // then compute.  Prefetches past the range load a dummy line instead, so
     // every path issues the same loads and the wait counts stay exact.
     TileRegs<D, FP8> r[DEPTH];
-    load_tile<D, WIDE, FP8>(r[0], p, win, win_base, t, end, true, lane, kvh);
+    load_tile<D, WIDE, FP8, NT>(r[0], p, win, win_base, t, end, true, lane, kvh);
 #pragma unroll
     for (int d = 1; d < DEPTH; ++d) {
         ensure_window(t + 16 * d);
-        load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * d, end, d < ntiles, lane, kvh);
+        load_tile<D, WIDE, FP8, NT>(r[d], p, win, win_base, t + 16 * d, end, d < ntiles, lane, kvh);
     }
     after();
     int k = 0;
@@ -1026,7 +1036,8 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
             // against 27.7 µs per partition that way.
             __builtin_amdgcn_sched_barrier(0);
             ensure_window(t + 16 * DEPTH);
-            load_tile<D, WIDE, FP8>(r[d], p, win, win_base, t + 16 * DEPTH, end, k + d + DEPTH < ntiles, lane, kvh);
+            load_tile<D, WIDE, FP8, NT>(r[d], p, win, win_base, t + 16 * DEPTH, end, k + d + DEPTH < ntiles, lane,
+                                        kvh);
             __builtin_amdgcn_sched_barrier(0);
             Math::tile(q, acc, lds, t, end, lane, scale_log2);
             t += 16;
@@ -1047,7 +1058,7 @@ __device__ __forceinline__ void tile_loop(const PartitionParams& p, const int32_
 // Attention of one head slice over tokens [begin, end) (begin < end), the page
 // window already loaded at some win_base <= begin / P.  Leaves Math's
 // accumulator (unnormalised O, reference max, denominator) finished.
-template <typename Math, int D, bool WIDE, int DEPTH, bool FP8, typename After = NoWork>
+template <typename Math, int D, bool WIDE, int DEPTH, bool FP8, bool NT = true, typename After = NoWork>
 __device__ __forceinline__ void attend_range(const PartitionParams& p, const int32_t* __restrict__ bt_row, int win,
                                              int win_base, const typename Math::Q& q, uint16_t* lds, int begin,
                                              int end, int lane, int kvh, typename Math::Acc& acc, float scale_log2,
@@ -1064,11 +1075,11 @@ __device__ __forceinline__ void attend_range(const PartitionParams& p, const int
     }
     if (last_page - win_base < 64) {
         // Common case: the whole range fits in one page window.
-        tile_loop<Math, D, WIDE, DEPTH, false, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
-                                                    lane, kvh, scale_log2, after);
+        tile_loop<Math, D, WIDE, DEPTH, false, FP8, NT>(p, bt_row, last_page, win, win_base, q, acc, lds, begin,
+                                                        end, lane, kvh, scale_log2, after);
     } else {
-        tile_loop<Math, D, WIDE, DEPTH, true, FP8>(p, bt_row, last_page, win, win_base, q, acc, lds, begin, end,
-                                                   lane, kvh, scale_log2, after);
+        tile_loop<Math, D, WIDE, DEPTH, true, FP8, NT>(p, bt_row, last_page, win, win_base, q, acc, lds, begin,
+                                                       end, lane, kvh, scale_log2, after);
     }
     Math::finish(acc);
 }
@@ -1266,7 +1277,7 @@ void partition_item_group_kernel(PartitionParams p) {
 // workgroup's LDS request is padded on the host so that one workgroup occupies
 // a CU: the dispatcher then spreads the grid over all CUs instead of doubling
 // some up while others idle.
-template <typename Math, int D, bool WIDE, int DEPTH, int WAVES, bool FP8>
+template <typename Math, int D, bool WIDE, int DEPTH, int WAVES, bool FP8, bool NT = true>
 __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_tiles[WAVES][2 * VTile<D>::kElems];
 
@@ -1357,8 +1368,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                                          : (((static_cast<int64_t>(g) + static_cast<int64_t>(b) * sps + u) << gs) + j) *
                                                p.part_heads;
                 if constexpr (kDefer) {
-                    attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh,
-                                                            acc, ks.score_log2, flush);
+                    attend_range<Math, D, WIDE, DEPTH, FP8, NT>(p, bt_row, win, win_base, q, lds, begin, end, lane,
+                                                                kvh, acc, ks.score_log2, flush);
                     pend_final = whole;
                     pend_at = at;
                     pend_q = q;
@@ -1367,8 +1378,8 @@ __global__ __launch_bounds__(64 * WAVES) void partition_tiles_kernel(PartitionPa
                     pend_scale = ks.out;
                     pending = true;
                 } else {
-                    attend_range<Math, D, WIDE, DEPTH, FP8>(p, bt_row, win, win_base, q, lds, begin, end, lane, kvh,
-                                                            acc, ks.score_log2);
+                    attend_range<Math, D, WIDE, DEPTH, FP8, NT>(p, bt_row, win, win_base, q, lds, begin, end, lane,
+                                                                kvh, acc, ks.score_log2);
                     if (whole) {
                         Math::write_final(p, q, at, heads_here, acc, lane, ks.out);
                     } else {
@@ -1425,6 +1436,15 @@ static void launch_tiles(const PartitionParams& p, hipStream_t stream, const Lau
     constexpr size_t kStatic = sizeof(uint16_t) * kWaves * 2 * VTile<D>::kElems;
     constexpr size_t kHalf = 80 * 1024;
     const size_t dyn = kStatic <= kHalf ? kHalf + 256 - kStatic : 0;
+    // Rows past 32 per KV head make several head groups, and a gang then holds
+    // waves of one KV head reading the same tokens: plain loads (load_chunk).
+    if constexpr (Math::kHeads == 32 && WIDE) {
+        if (p.head_groups > 1 && p.gang_shift > 0) {
+            launch_kernel(partition_tiles_kernel<Math, D, WIDE, kv_depth<FP8>(), kWaves, FP8, false>, dim3(blocks),
+                          dim3(64 * kWaves), dyn, stream, ev, p);
+            return;
+        }
+    }
     launch_kernel(partition_tiles_kernel<Math, D, WIDE, kv_depth<FP8>(), kWaves, FP8>, dim3(blocks),
                   dim3(64 * kWaves), dyn, stream, ev, p);
 }
