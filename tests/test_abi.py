@@ -546,3 +546,18 @@ def test_descriptor_layout_matches_the_header(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     assert got[0] == ctypes.sizeof(_lib.PkvDecodeDesc)
     assert got[1:] == [getattr(_lib.PkvDecodeDesc, f).offset for f in fields]
+
+
+def test_head_groups_share_a_gang_on_the_tile_schedule():
+    """More than 32 query rows per KV head (16 heads per KV head, four query tokens: 64 rows) make
+    two head groups of 32 rows, and the tile schedule puts both in one gang (its waves read the
+    same tokens, the case its plain-load kernel serves; tests/test_gpu_fp8.py and the C5 verify
+    step of tests/test_gpu_full_size_features.py run it).  The partial slots hold 32 rows for
+    twice the streams."""
+    align = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for kv in (pagedkv.PKV_KV_DTYPE_SAME, pagedkv.PKV_KV_DTYPE_FP8_E4M3):
+        d = base_desc(batch=4, num_heads=16, num_heads_k=1, head_dim=256, page_size=16, block_table_stride=256,
+                      max_seqlen=4000, dtype=pagedkv.PKV_DTYPE_F16, seqlen_q=4, causal=True, kv_dtype=kv)
+        assert pagedkv.schedule_for(d, 0) == pagedkv.PKV_SCHED_TILES
+        rows = (pagedkv.num_splits_for(d, 0) + 4 * 2) * 32  # (waves + B x 2 head groups) slots of 32 rows
+        assert pagedkv.workspace_size(d, 0) == align(rows * 256 * 4) + align(rows * 4)

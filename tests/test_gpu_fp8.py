@@ -71,6 +71,7 @@ CASES = [
     (2, 8, 2, 128, 4, [100, 61], 1, 1, False),              # pages smaller than a tile
     (3, 32, 8, 128, 64, [1000, 5, 2049], 1, 4, True),       # speculative verify on FP8
     (2, 48, 2, 64, 16, [400, 90], 0, 1, False),             # 24 heads per KV head: 32-row waves
+    (4, 16, 1, 256, 16, [3000, 2500, 4000, 100], 0, 4, True),  # 64 rows: two head groups in a gang
 ]
 
 
